@@ -1,0 +1,150 @@
+/*
+ * neuralzip_hip.h -- C ABI of libneuralzip_hip.so, the MI355X (gfx950)
+ * exponent-lane decompression path.
+ *
+ * This boundary replaces the reference's nanobind module `_huff0_cpp`
+ * (neuralzip/native/module.cpp:36-90) on the GPU path and the CuPy/NVRTC
+ * launcher (neuralzip/gpu/decoder.py:57-208). Conventions:
+ *   - plain pointers and sizes; no framework types;
+ *   - every buffer is caller-owned; the library never frees caller memory;
+ *   - int results: 0 on success, a negative nz_status on failure, with a
+ *     thread-local message from nz_last_error();
+ *   - host functions are re-entrant; nz_decode_launch is asynchronous and
+ *     ordered on the given HIP stream.
+ */
+#ifndef NEURALZIP_HIP_H
+#define NEURALZIP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NZ_ABI_VERSION 1
+
+enum nz_status {
+    NZ_OK = 0,
+    NZ_INVALID_ARGUMENT = -1,
+    NZ_INVALID_CODEBOOK = -2,
+    NZ_UNCODED_SYMBOL = -3,
+    NZ_LAYOUT_LIMIT = -4,
+    NZ_CORRUPT_STREAM = -5,
+    NZ_HIP_ERROR = -6,
+    NZ_OUT_OF_MEMORY = -7,
+};
+
+typedef struct nz_codebook nz_codebook;
+typedef struct nz_layout nz_layout;
+
+/* Device structures; layout documented in neuralzip_amd/csrc/nz_format.h. */
+typedef struct nz_frag_desc nz_frag_desc;   /* 64 bytes */
+typedef struct nz_tile nz_tile;             /* 16 bytes */
+typedef struct nz_work nz_work;             /* 16 bytes */
+
+const char* nz_last_error(void);
+int nz_abi_version(void);
+
+/* ---- code tables ------------------------------------------------------ */
+
+/* Builds a code table from a codebook payload: an NZM1 header (b"NZM1" +
+ * token lengths) with its pair vocabulary, or a Huff0 tree description
+ * (RFC 8878 4.2.1) with an empty vocabulary.
+ * Replaces: _huff0_cpp.export_code_table (binding_helpers.h:103-123,
+ * gpu_layout.h:7-17) and GPUCodebook.__post_init__ (gpu/inference.py:28-75). */
+int nz_codebook_create(const uint8_t* header, size_t header_size,
+                       const uint8_t* vocab, size_t vocab_size, nz_codebook** out);
+void nz_codebook_destroy(nz_codebook* codebook);
+
+/* Per-token code lengths and canonical code values (tokens 0..255 are
+ * bytes, 256+k is pair k). `capacity` is the array length.
+ * Replaces: the (lengths, codes, longest) tuple of export_code_table. */
+int nz_codebook_export(const nz_codebook* codebook, uint8_t* lengths, uint64_t* codes,
+                       uint32_t capacity, uint32_t* n_tokens, uint32_t* longest);
+
+/* The device LUT image (uint32 words). With out == NULL only *n_words is
+ * set. Replaces: GPUCodebook.decode_lut (gpu/inference.py:39-75). */
+int nz_codebook_lut(const nz_codebook* codebook, uint32_t* out, uint32_t capacity_words,
+                    uint32_t* n_words);
+
+/* ---- GPU layout encoding ----------------------------------------------- */
+
+typedef struct {
+    const uint8_t* src;            /* numel * element_size bytes (host)     */
+    uint64_t numel;
+    const nz_codebook* codebook;   /* NULL: the exponent lane stays raw     */
+    uint64_t out;                  /* element index in the output workspace */
+    uint32_t element_size;         /* 2 or 4                                */
+    uint32_t bit_reorder;
+    uint32_t mantissa_bits;
+    uint32_t exponent_bits;
+} nz_fragment_spec;
+
+typedef struct {
+    uint64_t packed_bytes;         /* bytes in the packed buffer            */
+    uint64_t bit_length;           /* Huffman bits (0 for raw fragments)    */
+    uint64_t bits_bytes;           /* bitstream bytes, ceil(bit_length/8)   */
+    uint64_t meta_bytes;           /* window metadata bytes (2 per window)  */
+    uint64_t lane_bytes;           /* raw lane bytes                        */
+    uint32_t n_windows;
+    uint32_t n_tiles;
+    uint32_t kind;                 /* 0 raw, 1 codes <= 32 bits, 2 longer   */
+    uint32_t reserved;
+} nz_fragment_info;
+
+typedef struct {
+    uint64_t packed_bytes;
+    uint64_t n_fragments;
+    uint64_t n_tiles;
+} nz_layout_totals;
+
+/* Encodes `count` fragments (one chunk each) on up to `threads` workers
+ * (0: hardware concurrency, at most 16). Codebooks must outlive the layout.
+ * Replaces: _huff0_cpp.encode_gpu_tensor (binding_helpers.h:125-195,
+ * gpu_layout.h:62-241) driven per chunk from gpu/inference.py:308-330. */
+int nz_layout_encode(const nz_fragment_spec* specs, size_t count, int threads, nz_layout** out);
+void nz_layout_destroy(nz_layout* layout);
+int nz_layout_totals_get(const nz_layout* layout, nz_layout_totals* totals);
+int nz_layout_fragment_info(const nz_layout* layout, size_t index, nz_fragment_info* info);
+
+/* Writes every fragment, in order, into `dst` (host memory that will be
+ * copied to device byte offset `dst_base`); fills one descriptor per
+ * fragment and all tiles in fragment order, tagging them with fragment
+ * index frag_base + i. lut_offsets[i] is the device byte offset of the LUT
+ * image of fragment i's codebook (ignored for raw fragments).
+ * Replaces: per-group uploads and descriptor tensors (gpu/inference.py:
+ * 382-432, decoder.py:130-191). */
+int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base,
+                   const uint64_t* lut_offsets, uint32_t frag_base,
+                   nz_frag_desc* descs, nz_tile* tiles);
+
+/* Splits tiles into workgroup ranges of one codebook and kind, aiming at
+ * about `target_groups` workgroups. Writes at most `capacity` items.
+ * Replaces: the block→group / block→local id tensors (decoder.py:168-179). */
+int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                 uint32_t target_groups, nz_work* work, uint32_t capacity, uint32_t* n_work);
+
+/* ---- decode ----------------------------------------------------------- */
+
+/* Decodes the tiles named by `work` (device arrays) into the output
+ * workspace `out` (device), on HIP stream `stream` (NULL: default stream).
+ * `base` is the packed device buffer. long_codes selects the variant for
+ * codes of 33..56 bits; element_size/bit_reorder select the word layout
+ * (2/1 bfloat16, 2/0 float16, 4/1 float32).
+ * Replaces: CuPyDecoder.decode_batch (decoder.py:193-208) launching
+ * decode_batched (gpu/cuda/decode.cu:323-381). */
+int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                     const nz_work* work, uint32_t n_work, int element_size, int bit_reorder,
+                     int long_codes, void* out, void* stream);
+
+/* CPU emulation of nz_decode_launch on host copies of the same arrays; a
+ * test hook for GPU-less hosts, never used by the runtime. */
+int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                      const nz_work* work, uint32_t n_work, int element_size, int bit_reorder,
+                      uint8_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

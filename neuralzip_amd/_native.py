@@ -1,0 +1,195 @@
+"""ctypes binding of libneuralzip_hip.so (declared in include/neuralzip_hip.h).
+
+The library must be built in-tree (``python -m neuralzip_amd.build`` or
+``__graft_entry__.build()``); importing the GPU path without it raises.
+"""
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIBRARY = Path(__file__).resolve().parent / "libneuralzip_hip.so"
+
+FRAG_DESC = np.dtype([("bits", "<u8"), ("meta", "<u8"), ("lanes", "<u8"), ("out", "<u8"), ("lut", "<u8"),
+                      ("bit_length", "<u8"), ("numel", "<u4"), ("lane_stride", "<u4"), ("kind", "<u4"),
+                      ("reserved", "<u4")])
+TILE = np.dtype([("frag", "<u4"), ("win0", "<u4"), ("out0", "<u4"), ("n_win", "<u2"), ("n_out", "<u2")])
+WORK = np.dtype([("tile0", "<u4"), ("tile1", "<u4"), ("lut_frag", "<u4"), ("kind", "<u4")])
+assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16
+
+KIND_RAW, KIND_SHORT, KIND_LONG = 0, 1, 2
+
+
+class NativeError(RuntimeError):
+    """A failure reported by libneuralzip_hip (message from nz_last_error)."""
+
+    def __init__(self, code, message):
+        super().__init__(message)
+        self.code = code
+
+
+class _FragmentSpec(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("numel", ctypes.c_uint64), ("codebook", ctypes.c_void_p),
+                ("out", ctypes.c_uint64), ("element_size", ctypes.c_uint32), ("bit_reorder", ctypes.c_uint32),
+                ("mantissa_bits", ctypes.c_uint32), ("exponent_bits", ctypes.c_uint32)]
+
+
+class _FragmentInfo(ctypes.Structure):
+    _fields_ = [("packed_bytes", ctypes.c_uint64), ("bit_length", ctypes.c_uint64), ("bits_bytes", ctypes.c_uint64),
+                ("meta_bytes", ctypes.c_uint64), ("lane_bytes", ctypes.c_uint64), ("n_windows", ctypes.c_uint32),
+                ("n_tiles", ctypes.c_uint32), ("kind", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class _Totals(ctypes.Structure):
+    _fields_ = [("packed_bytes", ctypes.c_uint64), ("n_fragments", ctypes.c_uint64), ("n_tiles", ctypes.c_uint64)]
+
+
+_lib = None
+EXPORTS = ("nz_last_error", "nz_abi_version", "nz_codebook_create", "nz_codebook_destroy", "nz_codebook_export",
+           "nz_codebook_lut", "nz_layout_encode", "nz_layout_destroy", "nz_layout_totals_get",
+           "nz_layout_fragment_info", "nz_layout_pack", "nz_plan_work", "nz_decode_launch", "nz_emulate_decode")
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise ImportError(f"{LIBRARY} is not built; run `python -m neuralzip_amd.build` first.")
+        L = ctypes.CDLL(str(LIBRARY))
+        vp, u32, u64, sz = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_size_t
+        L.nz_last_error.restype = ctypes.c_char_p
+        L.nz_codebook_create.argtypes = [vp, sz, vp, sz, ctypes.POINTER(vp)]
+        L.nz_codebook_destroy.argtypes = [vp]
+        L.nz_codebook_destroy.restype = None
+        L.nz_codebook_export.argtypes = [vp, vp, vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
+        L.nz_codebook_lut.argtypes = [vp, vp, u32, ctypes.POINTER(u32)]
+        L.nz_layout_encode.argtypes = [vp, sz, ctypes.c_int, ctypes.POINTER(vp)]
+        L.nz_layout_destroy.argtypes = [vp]
+        L.nz_layout_destroy.restype = None
+        L.nz_layout_totals_get.argtypes = [vp, ctypes.POINTER(_Totals)]
+        L.nz_layout_fragment_info.argtypes = [vp, sz, ctypes.POINTER(_FragmentInfo)]
+        L.nz_layout_pack.argtypes = [vp, vp, u64, vp, u32, vp, vp]
+        L.nz_plan_work.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32)]
+        L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise NativeError(rc, lib().nz_last_error().decode())
+    return rc
+
+
+def _ptr(data):
+    """Address of a contiguous readable buffer (bytes, bytearray, memoryview, ndarray)."""
+    if isinstance(data, np.ndarray):
+        return data.ctypes.data
+    arr = np.frombuffer(data, dtype=np.uint8)
+    return arr.ctypes.data if arr.size else None
+
+
+class Codebook:
+    """Host code table + device LUT image of one codebook payload."""
+
+    def __init__(self, header, vocab=b""):
+        header = np.frombuffer(bytes(header), dtype=np.uint8)
+        vocab = np.frombuffer(bytes(vocab), dtype=np.uint8)
+        handle = ctypes.c_void_p()
+        check(lib().nz_codebook_create(header.ctypes.data if header.size else None, header.size,
+                                       vocab.ctypes.data if vocab.size else None, vocab.size,
+                                       ctypes.byref(handle)))
+        self.handle = handle.value
+        n, longest = ctypes.c_uint32(), ctypes.c_uint32()
+        check(lib().nz_codebook_export(self.handle, None, None, 0, ctypes.byref(n), ctypes.byref(longest)))
+        self.n_tokens, self.longest = n.value, longest.value
+
+    def __del__(self):
+        if getattr(self, "handle", None) and _lib is not None:
+            _lib.nz_codebook_destroy(self.handle)
+            self.handle = None
+
+    def export(self):
+        lengths = np.zeros(self.n_tokens, dtype=np.uint8)
+        codes = np.zeros(self.n_tokens, dtype=np.uint64)
+        check(lib().nz_codebook_export(self.handle, lengths.ctypes.data, codes.ctypes.data, self.n_tokens,
+                                       None, None))
+        return lengths, codes
+
+    def lut(self):
+        n = ctypes.c_uint32()
+        check(lib().nz_codebook_lut(self.handle, None, 0, ctypes.byref(n)))
+        out = np.zeros(n.value, dtype=np.uint32)
+        check(lib().nz_codebook_lut(self.handle, out.ctypes.data, n.value, None))
+        return out
+
+
+class Layout:
+    """Encoded fragments in host memory (one chunk each)."""
+
+    def __init__(self, fragments, threads=0):
+        """fragments: iterable of (src ndarray/bytes, codebook or None, out offset, DTypeSpec-like)."""
+        self._keep = []
+        specs = []
+        for src, codebook, out, dtype in fragments:
+            arr = np.ascontiguousarray(np.frombuffer(src, dtype=np.uint8) if not isinstance(src, np.ndarray)
+                                       else src.reshape(-1).view(np.uint8))
+            self._keep.append(arr)
+            if codebook is not None:
+                self._keep.append(codebook)
+            specs.append(_FragmentSpec(arr.ctypes.data, arr.size // dtype.element_size,
+                                       codebook.handle if codebook is not None else None, int(out),
+                                       dtype.element_size, int(dtype.bit_reorder), dtype.mantissa_bits,
+                                       dtype.exponent_mask.bit_length()))
+        array = (_FragmentSpec * max(len(specs), 1))(*specs)
+        handle = ctypes.c_void_p()
+        check(lib().nz_layout_encode(ctypes.cast(array, ctypes.c_void_p), len(specs), int(threads),
+                                     ctypes.byref(handle)))
+        self.handle = handle.value
+        totals = _Totals()
+        check(lib().nz_layout_totals_get(self.handle, ctypes.byref(totals)))
+        self.packed_bytes, self.n_fragments, self.n_tiles = (totals.packed_bytes, totals.n_fragments,
+                                                             totals.n_tiles)
+        self._keep = [k for k in self._keep if isinstance(k, Codebook)]   # sources no longer needed
+
+    def __del__(self):
+        if getattr(self, "handle", None) and _lib is not None:
+            _lib.nz_layout_destroy(self.handle)
+            self.handle = None
+
+    def info(self, index):
+        info = _FragmentInfo()
+        check(lib().nz_layout_fragment_info(self.handle, index, ctypes.byref(info)))
+        return {name: getattr(info, name) for name, _ in _FragmentInfo._fields_}
+
+    def pack(self, dst, dst_base, lut_offsets, frag_base=0):
+        """Writes all fragments into `dst` (uint8 ndarray view of host memory
+        that lands at device offset dst_base); returns (descs, tiles)."""
+        descs = np.zeros(self.n_fragments, dtype=FRAG_DESC)
+        tiles = np.zeros(self.n_tiles, dtype=TILE)
+        luts = np.ascontiguousarray(lut_offsets, dtype=np.uint64)
+        check(lib().nz_layout_pack(self.handle, dst.ctypes.data, int(dst_base), luts.ctypes.data,
+                                   int(frag_base), descs.ctypes.data, tiles.ctypes.data))
+        return descs, tiles
+
+
+def plan_work(descs, tiles, target_groups):
+    n = ctypes.c_uint32()
+    check(lib().nz_plan_work(descs.ctypes.data, tiles.ctypes.data if len(tiles) else None, len(tiles),
+                             int(target_groups), None, 0, ctypes.byref(n)))
+    work = np.zeros(n.value, dtype=WORK)
+    check(lib().nz_plan_work(descs.ctypes.data, tiles.ctypes.data if len(tiles) else None, len(tiles),
+                             int(target_groups), work.ctypes.data, n.value, ctypes.byref(n)))
+    return work
+
+
+def decode_launch(base_ptr, frags_ptr, tiles_ptr, work_ptr, n_work, element_size, bit_reorder, long_codes,
+                  out_ptr, stream_ptr):
+    check(lib().nz_decode_launch(base_ptr, frags_ptr, tiles_ptr, work_ptr, int(n_work), int(element_size),
+                                 int(bit_reorder), int(long_codes), out_ptr, stream_ptr))
+
+
+def emulate_decode(base, descs, tiles, work, element_size, bit_reorder, out):
+    check(lib().nz_emulate_decode(base.ctypes.data, descs.ctypes.data, tiles.ctypes.data, work.ctypes.data,
+                                  len(work), int(element_size), int(bit_reorder), out.ctypes.data))

@@ -1,0 +1,249 @@
+// capi.cpp -- extern "C" boundary of libneuralzip_hip.so (include/neuralzip_hip.h).
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <new>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "codebook.hpp"
+#include "layout.hpp"
+#include "neuralzip_hip.h"
+#include "nz_format.h"
+
+struct nz_codebook {
+    nz::Codebook book;
+};
+
+struct nz_layout {
+    std::vector<nz::Fragment> fragments;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int set_error(int code, const char* message) {
+    g_error = message;
+    return code;
+}
+
+template <typename F>
+int guarded(F&& body) {
+    try {
+        body();
+        return 0;
+    } catch (const nz::Error& e) {
+        return set_error(e.code, e.what());
+    } catch (const std::bad_alloc&) {
+        return set_error(nz::kOutOfMemory, "Out of host memory.");
+    } catch (const std::exception& e) {
+        return set_error(nz::kInvalidArgument, e.what());
+    } catch (...) {
+        return set_error(nz::kInvalidArgument, "Unknown native failure.");
+    }
+}
+
+// run_parallel_jobs (neuralzip/native/common.h:134-185): at most 16
+// workers, one when the input is small; the first error wins.
+template <typename Job>
+void parallel_for(size_t count, size_t total_bytes, int threads, Job&& job) {
+    unsigned hw = std::thread::hardware_concurrency();
+    int workers = threads > 0 ? threads : static_cast<int>(hw ? hw : 1);
+    workers = std::max(1, std::min<int>({workers, 16, static_cast<int>(std::max<size_t>(count, 1))}));
+    if (total_bytes < (512u << 10)) workers = 1;
+    std::vector<std::string> errors(count);
+    std::vector<int> codes(count, 0);
+    std::atomic<size_t> next{0};
+    auto worker = [&]() {
+        for (size_t i; (i = next.fetch_add(1)) < count;) {
+            try {
+                job(i);
+            } catch (const nz::Error& e) {
+                errors[i] = e.what();
+                codes[i] = e.code;
+            } catch (const std::exception& e) {
+                errors[i] = e.what();
+                codes[i] = nz::kInvalidArgument;
+            }
+        }
+    };
+    if (workers == 1) {
+        worker();
+    } else {
+        std::vector<std::thread> pool;
+        for (int w = 0; w < workers; ++w) pool.emplace_back(worker);
+        for (auto& t : pool) t.join();
+    }
+    for (size_t i = 0; i < count; ++i)
+        if (codes[i]) throw nz::Error(codes[i], errors[i]);
+}
+
+}  // namespace
+
+extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* work,
+                                    uint32_t n_work, int element_size, int bit_reorder, int long_codes,
+                                    void* out, void* stream, char* message, size_t message_size);
+
+extern "C" {
+
+const char* nz_last_error(void) { return g_error.c_str(); }
+
+int nz_abi_version(void) { return 1; }
+
+int nz_codebook_create(const uint8_t* header, size_t header_size, const uint8_t* vocab, size_t vocab_size,
+                       nz_codebook** out) {
+    return guarded([&] {
+        if (!out || (!header && header_size)) nz::fail(nz::kInvalidArgument, "Null codebook argument.");
+        auto book = std::make_unique<nz_codebook>();
+        book->book = nz::build_codebook(header, header_size, vocab, vocab_size);
+        *out = book.release();
+    });
+}
+
+void nz_codebook_destroy(nz_codebook* codebook) { delete codebook; }
+
+int nz_codebook_export(const nz_codebook* c, uint8_t* lengths, uint64_t* codes, uint32_t capacity,
+                       uint32_t* n_tokens, uint32_t* longest) {
+    return guarded([&] {
+        if (!c) nz::fail(nz::kInvalidArgument, "Null codebook.");
+        const uint32_t n = c->book.token_count();
+        if (n_tokens) *n_tokens = n;
+        if (longest) *longest = c->book.longest;
+        if (lengths || codes) {
+            if (capacity < n) nz::fail(nz::kInvalidArgument, "Export arrays are too small.");
+            for (uint32_t t = 0; t < n; ++t) {
+                if (lengths) lengths[t] = c->book.lengths[t];
+                if (codes) codes[t] = c->book.lengths[t] ? c->book.codes[t] : 0;
+            }
+        }
+    });
+}
+
+int nz_codebook_lut(const nz_codebook* c, uint32_t* out, uint32_t capacity_words, uint32_t* n_words) {
+    return guarded([&] {
+        if (!c) nz::fail(nz::kInvalidArgument, "Null codebook.");
+        const auto& lut = c->book.lut;
+        if (n_words) *n_words = static_cast<uint32_t>(lut.size());
+        if (out) {
+            if (capacity_words < lut.size()) nz::fail(nz::kInvalidArgument, "LUT buffer is too small.");
+            std::memcpy(out, lut.data(), lut.size() * 4);
+        }
+    });
+}
+
+int nz_layout_encode(const nz_fragment_spec* specs, size_t count, int threads, nz_layout** out) {
+    return guarded([&] {
+        if (!out || (!specs && count)) nz::fail(nz::kInvalidArgument, "Null layout argument.");
+        if (threads < 0) nz::fail(nz::kInvalidArgument, "threads must be non-negative.");
+        auto layout = std::make_unique<nz_layout>();
+        layout->fragments.resize(count);
+        size_t total = 0;
+        for (size_t i = 0; i < count; ++i) {
+            if (specs[i].numel > 0xFFFFFFFFull) nz::fail(nz::kLayoutLimit, "Fragment exceeds 2^32 elements.");
+            if (!specs[i].src) nz::fail(nz::kInvalidArgument, "Null fragment source.");
+            total += specs[i].numel * specs[i].element_size;
+        }
+        parallel_for(count, total, threads, [&](size_t i) {
+            const nz_fragment_spec& s = specs[i];
+            nz::LaneSpec lane{s.element_size, s.bit_reorder != 0, s.mantissa_bits, s.exponent_bits};
+            layout->fragments[i] = nz::encode_fragment(s.src, static_cast<uint32_t>(s.numel), s.out, lane,
+                                                       s.codebook ? &s.codebook->book : nullptr);
+        });
+        *out = layout.release();
+    });
+}
+
+void nz_layout_destroy(nz_layout* layout) { delete layout; }
+
+int nz_layout_totals_get(const nz_layout* layout, nz_layout_totals* totals) {
+    return guarded([&] {
+        if (!layout || !totals) nz::fail(nz::kInvalidArgument, "Null layout argument.");
+        totals->packed_bytes = 0;
+        totals->n_tiles = 0;
+        totals->n_fragments = layout->fragments.size();
+        for (const auto& f : layout->fragments) {
+            totals->packed_bytes += nz::packed_size(f);
+            totals->n_tiles += f.tiles.size();
+        }
+    });
+}
+
+int nz_layout_fragment_info(const nz_layout* layout, size_t index, nz_fragment_info* info) {
+    return guarded([&] {
+        if (!layout || !info || index >= layout->fragments.size())
+            nz::fail(nz::kInvalidArgument, "Fragment index out of range.");
+        const nz::Fragment& f = layout->fragments[index];
+        info->packed_bytes = nz::packed_size(f);
+        info->bit_length = f.bit_length;
+        info->bits_bytes = f.book ? (f.bit_length + 7) / 8 : f.numel;
+        info->meta_bytes = f.meta.size() * 2;
+        info->lane_bytes = static_cast<uint64_t>(f.spec.element_size - 1) * f.numel;
+        info->n_windows = f.n_windows;
+        info->n_tiles = static_cast<uint32_t>(f.tiles.size());
+        info->kind = f.kind;
+        info->reserved = 0;
+    });
+}
+
+int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base, const uint64_t* lut_offsets,
+                   uint32_t frag_base, nz_frag_desc* descs, nz_tile* tiles) {
+    return guarded([&] {
+        if (!layout || !dst || !descs || !tiles) nz::fail(nz::kInvalidArgument, "Null pack argument.");
+        if (dst_base % 16) nz::fail(nz::kInvalidArgument, "Packed destination must be 16-byte aligned.");
+        uint64_t cursor = 0;
+        size_t t = 0;
+        for (size_t i = 0; i < layout->fragments.size(); ++i) {
+            const nz::Fragment& f = layout->fragments[i];
+            if (f.book && (!lut_offsets || lut_offsets[i] % 16))
+                nz::fail(nz::kInvalidArgument, "LUT images must be 16-byte aligned.");
+            nz::pack_fragment(f, dst + cursor, 0, f.book ? lut_offsets[i] : 0, &descs[i]);
+            descs[i].bits += dst_base + cursor;
+            descs[i].meta += dst_base + cursor;
+            descs[i].lanes += dst_base + cursor;
+            cursor += nz::packed_size(f);
+            for (const nz_tile& tile : f.tiles) {
+                tiles[t] = tile;
+                tiles[t].frag = frag_base + static_cast<uint32_t>(i);
+                ++t;
+            }
+        }
+    });
+}
+
+int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t target_groups,
+                 nz_work* work, uint32_t capacity, uint32_t* n_work) {
+    return guarded([&] {
+        if (!frags || (!tiles && n_tiles) || !n_work) nz::fail(nz::kInvalidArgument, "Null plan argument.");
+        const auto plan = nz::plan_work(frags, tiles, n_tiles, target_groups);
+        *n_work = static_cast<uint32_t>(plan.size());
+        if (work) {
+            if (plan.size() > capacity) nz::fail(nz::kInvalidArgument, "Work buffer is too small.");
+            std::copy(plan.begin(), plan.end(), work);
+        }
+    });
+}
+
+int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* work,
+                     uint32_t n_work, int element_size, int bit_reorder, int long_codes, void* out, void* stream) {
+    char message[256] = {0};
+    const int rc = nz_hip_decode_launch(base, frags, tiles, work, n_work, element_size, bit_reorder, long_codes,
+                                        out, stream, message, sizeof message);
+    if (rc) return set_error(rc, message);
+    return 0;
+}
+
+int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* work,
+                      uint32_t n_work, int element_size, int bit_reorder, uint8_t* out) {
+    return guarded([&] {
+        if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
+        nz::emulate_decode(base, frags, tiles, work, n_work, static_cast<unsigned>(element_size), bit_reorder != 0,
+                           out);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// codebook.hpp -- host-side code tables for the GPU decode path.
+#pragma once
+#include <array>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace nz {
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& message) : std::runtime_error(message), code(c) {}
+};
+
+enum ErrorCode : int {
+    kInvalidArgument = -1,
+    kInvalidCodebook = -2,
+    kUncodedSymbol = -3,
+    kLayoutLimit = -4,
+    kCorruptStream = -5,
+    kHipError = -6,
+    kOutOfMemory = -7,
+};
+
+[[noreturn]] inline void fail(int code, const std::string& message) { throw Error(code, message); }
+
+// One prefix code over tokens 0..255 (single exponent bytes) and 256+k
+// (pair k of the vocabulary, two bytes), with canonical code values:
+// tokens sorted by (length, token) receive consecutive codes, shortest first
+// (the NZM1 convention of neuralzip/native/mixed_huffman.h:42-70, applied to
+// singleton Huff0 tables too; the GPU layout is free to choose its codes).
+struct Codebook {
+    bool mixed = false;                 // NZM1 header (pairs allowed)
+    std::vector<uint8_t> lengths;       // per token; 0 = no code
+    std::vector<uint64_t> codes;        // canonical, valid where length > 0
+    std::vector<uint16_t> token_bytes;  // singleton s -> s; pair -> b0 | b1 << 8
+    std::vector<uint16_t> pair_token;   // 65536 entries, 0 = not a pair
+    unsigned longest = 0;
+    std::vector<uint32_t> lut;          // device LUT image (nz_format.h)
+    uint64_t vocab_bytes = 0;
+
+    unsigned token_count() const { return static_cast<unsigned>(lengths.size()); }
+    static unsigned token_width(unsigned token) { return token < 256 ? 1u : 2u; }
+};
+
+// Parses either an NZM1 header (b"NZM1" + token lengths, with vocab holding
+// the pairs) or a Huff0 tree description (RFC 8878 4.2.1). Mirrors the
+// validation of make_mixed_table (mixed_huffman.h:5-57) and HUF_readCTable.
+Codebook build_codebook(const uint8_t* header, size_t header_size,
+                        const uint8_t* vocab, size_t vocab_size);
+
+// Huffman weights of a Huff0 tree description: returns the code lengths of
+// symbols 0..255 (0 = absent) and the description's byte size.
+std::array<uint8_t, 256> huff0_lengths(const uint8_t* header, size_t size, size_t* used);
+
+// Decoder step at the head of a 64-bit window (MSB first): returns consumed
+// bits and writes the emitted bytes (1..3) into *bytes / *count. Uses the
+// LUT image exactly as the kernel does.
+unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* bytes,
+                  unsigned* count);
+
+}  // namespace nz

@@ -1,0 +1,300 @@
+// layout.cpp -- encodes chunks into the wave64 GPU layout (nz_format.h),
+// packs them, partitions tiles into workgroups, and emulates the kernel.
+//
+// Replaces the reference's GPU layout encoder (gpu_layout.h:62-241) and the
+// launcher's descriptor construction (decoder.py:130-191).
+#include "layout.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+namespace nz {
+namespace {
+
+uint32_t load_word(const uint8_t* p, unsigned es) {
+    uint32_t v = 0;
+    for (unsigned k = 0; k < es; ++k) v |= static_cast<uint32_t>(p[k]) << (8 * k);
+    return v;
+}
+
+// neuralzip/dtypes.py:23-45; only the byte-aligned exponent layouts reorder.
+uint32_t reorder_forward(uint32_t v, unsigned m, unsigned e) {
+    return (v & ((1u << m) - 1u)) | ((v >> e) & (1u << m)) | ((v << 1) & (((1u << e) - 1u) << (m + 1)));
+}
+
+uint32_t reorder_restore(uint32_t v, unsigned m, unsigned e) {
+    return (v & ((1u << m) - 1u)) | ((v << e) & (1u << (m + e))) | ((v >> 1) & (((1u << e) - 1u) << m));
+}
+
+// 64 bits of an MSB-first stream starting at bit `pos` (the buffer carries
+// enough zero padding after the last window).
+uint64_t peek64(const uint8_t* bits, uint64_t pos) {
+    const uint8_t* p = bits + (pos >> 3);
+    uint64_t v = 0;
+    for (int i = 0; i < 8; ++i) v = (v << 8) | p[i];
+    const unsigned r = pos & 7;
+    return r ? (v << r) | (p[8] >> (8 - r)) : v;
+}
+
+uint32_t alignbit(uint32_t a, uint32_t b, uint32_t s) {
+    return static_cast<uint32_t>(((static_cast<uint64_t>(a) << 32) | b) >> (s & 31));
+}
+
+uint32_t load_be32(const uint8_t* p) {
+    return (uint32_t(p[0]) << 24) | (uint32_t(p[1]) << 16) | (uint32_t(p[2]) << 8) | p[3];
+}
+
+}  // namespace
+
+Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const LaneSpec& spec,
+                         const Codebook* book) {
+    const unsigned es = spec.element_size;
+    if (es != 2 && es != 4) fail(kInvalidArgument, "GPU element_size must be 2 or 4.");
+    if (spec.bit_reorder && !(spec.exponent_bits == 8 && spec.mantissa_bits == es * 8 - 9))
+        fail(kInvalidArgument, "Reordered layouts need a byte-aligned 8-bit exponent.");
+    if (spec.mantissa_bits + spec.exponent_bits + 1 != es * 8)
+        fail(kInvalidArgument, "Sign, exponent and mantissa fields must fill the element.");
+    if (numel == 0) fail(kInvalidArgument, "A fragment needs at least one element.");
+    Fragment f;
+    f.numel = numel;
+    f.out = out;
+    f.spec = spec;
+    f.book = book;
+    const uint32_t V = nz_vector_elements(static_cast<int>(es));
+    const uint32_t pad = static_cast<uint32_t>(out % V);
+    f.lane_stride = static_cast<uint32_t>(align16(pad + numel));
+    f.lanes.assign(static_cast<size_t>(es - 1) * f.lane_stride, 0);
+    std::vector<uint8_t> sym(numel);
+    for (uint32_t i = 0; i < numel; ++i) {
+        uint32_t v = load_word(src + static_cast<size_t>(i) * es, es);
+        if (spec.bit_reorder) v = reorder_forward(v, spec.mantissa_bits, spec.exponent_bits);
+        sym[i] = static_cast<uint8_t>(v >> (8 * (es - 1)));
+        for (unsigned k = 0; k + 1 < es; ++k)
+            f.lanes[static_cast<size_t>(k) * f.lane_stride + pad + i] = static_cast<uint8_t>(v >> (8 * k));
+    }
+    if (!book) {
+        f.kind = NZ_KIND_RAW;
+        f.bits.assign(f.lane_stride, 0);
+        std::memcpy(f.bits.data() + pad, sym.data(), numel);
+        for (uint32_t start = 0; start < numel;) {
+            const uint32_t end = std::min<uint32_t>(numel, (start + pad) / NZ_RAW_TILE * NZ_RAW_TILE + NZ_RAW_TILE - pad);
+            f.tiles.push_back({0, 0, start, 0, static_cast<uint16_t>(end - start)});
+            start = end;
+        }
+        return f;
+    }
+    f.kind = book->longest > 32 ? NZ_KIND_LONG : NZ_KIND_SHORT;
+    // greedy pair parse (gpu_layout.h:232-239, mixed_huffman.h:85-94)
+    std::vector<uint16_t> tokens;
+    tokens.reserve(numel);
+    uint64_t bit_length = 0;
+    for (uint32_t i = 0; i < numel;) {
+        unsigned token = sym[i];
+        if (book->mixed && i + 1 < numel) {
+            const unsigned pair = book->pair_token[sym[i] | (static_cast<unsigned>(sym[i + 1]) << 8)];
+            if (pair) token = pair;
+        }
+        const unsigned length = book->lengths[token];
+        if (!length)
+            fail(kUncodedSymbol, "Symbol " + std::to_string(token) + " at index " + std::to_string(i) +
+                                     " has no codebook entry.");
+        tokens.push_back(static_cast<uint16_t>(token));
+        bit_length += length;
+        i += Codebook::token_width(token);
+    }
+    f.bit_length = bit_length;
+    const uint64_t n_windows = (bit_length + NZ_WINDOW_BITS - 1) / NZ_WINDOW_BITS;
+    if (n_windows > 0xFFFFFFFFull) fail(kLayoutLimit, "Fragment bitstream too long.");
+    f.n_windows = static_cast<uint32_t>(n_windows);
+    f.bits.assign(8 * n_windows + NZ_BITS_PAD, 0);
+    {
+        uint64_t acc = 0;
+        unsigned pending = 0;
+        size_t cursor = 0;
+        for (uint16_t t : tokens) {
+            const unsigned len = book->lengths[t];
+            const uint64_t code = book->codes[t];
+            // append `len` bits, most significant first, flushing whole bytes
+            for (unsigned done = 0; done < len;) {
+                const unsigned take = std::min(len - done, 56u - pending);
+                const uint64_t part = (code >> (len - done - take)) & ((uint64_t(1) << take) - 1);
+                acc = (acc << take) | part;
+                pending += take;
+                done += take;
+                while (pending >= 8) {
+                    pending -= 8;
+                    f.bits[cursor++] = static_cast<uint8_t>(acc >> pending);
+                }
+                acc &= pending ? (uint64_t(1) << pending) - 1 : 0;
+            }
+        }
+        if (pending) f.bits[cursor++] = static_cast<uint8_t>(acc << (8 - pending));
+    }
+    // simulate the kernel's step sequence to place window boundaries
+    f.meta.resize(n_windows);
+    std::vector<uint32_t> counts(n_windows);
+    uint64_t pos = 0, total = 0;
+    for (uint64_t w = 0; w < n_windows; ++w) {
+        const uint64_t gap = pos - w * NZ_WINDOW_BITS;
+        if (gap > 255) fail(kLayoutLimit, "Window gap exceeds its byte.");
+        const uint64_t end = std::min<uint64_t>((w + 1) * NZ_WINDOW_BITS, bit_length);
+        uint32_t count = 0;
+        while (pos < end) {
+            uint32_t bytes;
+            unsigned n;
+            pos += lut_step(book->lut, peek64(f.bits.data(), pos), &bytes, &n);
+            count += n;
+        }
+        if (count > 255) fail(kLayoutLimit, "Window count exceeds its byte.");
+        f.meta[w] = static_cast<uint16_t>(gap | (count << 8));
+        counts[w] = count;
+        total += count;
+    }
+    if (total < numel) fail(kCorruptStream, "Layout simulation emitted fewer bytes than elements.");
+    // group windows into wavefront tiles
+    uint64_t out0 = 0;
+    for (uint64_t w = 0; w < n_windows;) {
+        uint64_t end = w, sum = 0;
+        while (end < n_windows && end - w < NZ_WAVE && sum + counts[end] <= NZ_TILE_OUT) sum += counts[end++];
+        if (end == w) fail(kLayoutLimit, "A window exceeds the tile staging capacity.");
+        const uint64_t n_out = std::min<uint64_t>(sum, numel - std::min<uint64_t>(out0, numel));
+        if (n_out == 0) fail(kCorruptStream, "Empty tile in layout.");
+        f.tiles.push_back({0, static_cast<uint32_t>(w), static_cast<uint32_t>(out0),
+                           static_cast<uint16_t>(end - w), static_cast<uint16_t>(n_out)});
+        out0 += sum;
+        w = end;
+    }
+    return f;
+}
+
+uint64_t packed_size(const Fragment& f) {
+    return align16(f.bits.size()) + align16(f.meta.size() * 2) + f.lanes.size();
+}
+
+void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lut_offset, nz_frag_desc* d) {
+    uint64_t cursor = offset;
+    std::memcpy(dst + cursor, f.bits.data(), f.bits.size());
+    std::memset(dst + cursor + f.bits.size(), 0, align16(f.bits.size()) - f.bits.size());
+    d->bits = cursor;
+    cursor += align16(f.bits.size());
+    if (!f.meta.empty()) std::memcpy(dst + cursor, f.meta.data(), f.meta.size() * 2);
+    std::memset(dst + cursor + f.meta.size() * 2, 0, align16(f.meta.size() * 2) - f.meta.size() * 2);
+    d->meta = cursor;
+    cursor += align16(f.meta.size() * 2);
+    if (!f.lanes.empty()) std::memcpy(dst + cursor, f.lanes.data(), f.lanes.size());
+    d->lanes = cursor;
+    d->out = f.out;
+    d->lut = f.book ? lut_offset : 0;
+    d->bit_length = f.bit_length;
+    d->numel = f.numel;
+    d->lane_stride = f.lane_stride;
+    d->kind = f.kind;
+    d->reserved = 0;
+}
+
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                               uint32_t target_groups) {
+    std::vector<nz_work> work;
+    if (!n_tiles) return work;
+    const uint32_t per = std::max<uint32_t>(1, (n_tiles + std::max<uint32_t>(target_groups, 1) - 1) /
+                                                   std::max<uint32_t>(target_groups, 1));
+    auto key = [&](uint32_t t) {
+        const nz_frag_desc& f = frags[tiles[t].frag];
+        return std::pair<uint64_t, uint32_t>(f.kind == NZ_KIND_RAW ? 0 : f.lut, f.kind);
+    };
+    uint32_t start = 0;
+    for (uint32_t t = 1; t <= n_tiles; ++t) {
+        if (t == n_tiles || t - start >= per || key(t) != key(start)) {
+            work.push_back({start, t, tiles[start].frag, frags[tiles[start].frag].kind});
+            start = t;
+        }
+    }
+    return work;
+}
+
+namespace {
+
+void put_element(uint8_t* out, uint64_t g, unsigned es, bool reorder, uint32_t v) {
+    if (reorder) v = reorder_restore(v, es * 8 - 9, 8);
+    for (unsigned k = 0; k < es; ++k) out[g * es + k] = static_cast<uint8_t>(v >> (8 * k));
+}
+
+uint32_t lane_bytes(const uint8_t* base, const nz_frag_desc& f, uint64_t g, unsigned es, uint8_t expo) {
+    const uint64_t V = nz_vector_elements(static_cast<int>(es));
+    const uint64_t idx = g - f.out / V * V;
+    uint32_t v = static_cast<uint32_t>(expo) << (8 * (es - 1));
+    for (unsigned k = 0; k + 1 < es; ++k) v |= static_cast<uint32_t>(base[f.lanes + k * f.lane_stride + idx]) << (8 * k);
+    return v;
+}
+
+}  // namespace
+
+void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                    const nz_work* work, uint32_t n_work, unsigned es, bool reorder, uint8_t* out) {
+    const uint64_t V = nz_vector_elements(static_cast<int>(es));
+    std::vector<uint8_t> stage(NZ_TILE_OUT + 32);
+    for (uint32_t wi = 0; wi < n_work; ++wi) {
+        // the workgroup stages the LUT of work[wi].lut_frag
+        const nz_frag_desc& lf = frags[work[wi].lut_frag];
+        std::vector<uint32_t> lut;
+        if (work[wi].kind != NZ_KIND_RAW) {
+            const uint32_t* img = reinterpret_cast<const uint32_t*>(base + lf.lut);
+            lut.assign(img, img + img[2]);
+        }
+        for (uint32_t t = work[wi].tile0; t < work[wi].tile1; ++t) {
+            const nz_tile& tile = tiles[t];
+            const nz_frag_desc& f = frags[tile.frag];
+            const uint64_t A0 = f.out + tile.out0, A1 = A0 + tile.n_out;
+            if (f.kind == NZ_KIND_RAW) {
+                for (uint64_t g = A0; g < A1; ++g) {
+                    const uint8_t e = base[f.bits + (g - f.out / V * V)];
+                    put_element(out, g, es, reorder, lane_bytes(base, f, g, es, e));
+                }
+                continue;
+            }
+            const bool longmode = f.kind == NZ_KIND_LONG;
+            // wavefront exclusive scan of counts
+            uint32_t offset[NZ_WAVE] = {0};
+            for (unsigned l = 1; l < tile.n_win; ++l)
+                offset[l] = offset[l - 1] + (base[f.meta + 2 * (tile.win0 + l - 1) + 1]);
+            const uint64_t s0 = A0 - A0 / V * V;
+            std::fill(stage.begin(), stage.end(), 0xA5);
+            for (unsigned l = 0; l < tile.n_win; ++l) {
+                const uint64_t w = tile.win0 + l;
+                const unsigned gap = base[f.meta + 2 * w];
+                const uint8_t* src = base + f.bits + 8 * w;
+                uint32_t hi = load_be32(src), mid = load_be32(src + 4), lo = load_be32(src + 8);
+                uint32_t la = longmode ? load_be32(src + 12) : 0;
+                const uint64_t end = std::min<uint64_t>(64, f.bit_length - 64 * w);
+                auto shift = [&](unsigned len) {
+                    if (len >= 32) { hi = mid; mid = lo; lo = la; la = 0; len -= 32; }
+                    if (len) {
+                        const uint32_t s = 32 - len;
+                        hi = alignbit(hi, mid, s);
+                        mid = alignbit(mid, lo, s);
+                        lo = alignbit(lo, la, s);
+                        la = alignbit(la, 0, s);
+                    }
+                };
+                shift(gap);
+                uint64_t pos = gap;
+                uint64_t o = s0 + offset[l];
+                while (pos < end) {
+                    const uint64_t window = (static_cast<uint64_t>(hi) << 32) | mid;
+                    uint32_t bytes;
+                    unsigned n;
+                    const unsigned len = lut_step(lut, window, &bytes, &n);
+                    for (unsigned b = 0; b < n; ++b) stage.at(o + b) = static_cast<uint8_t>(bytes >> (8 * b));
+                    o += n;
+                    shift(len);
+                    pos += len;
+                }
+            }
+            for (uint64_t g = A0; g < A1; ++g)
+                put_element(out, g, es, reorder, lane_bytes(base, f, g, es, stage[g - A0 / V * V]));
+        }
+    }
+}
+
+}  // namespace nz

@@ -1,0 +1,64 @@
+// layout.hpp -- host encoder of the wave64 GPU layout.
+#pragma once
+#include <cstdint>
+#include <vector>
+
+#include "codebook.hpp"
+#include "nz_format.h"
+
+namespace nz {
+
+struct LaneSpec {
+    unsigned element_size = 2;
+    bool bit_reorder = true;
+    unsigned mantissa_bits = 7;
+    unsigned exponent_bits = 8;
+};
+
+// One encoded fragment in host memory.
+struct Fragment {
+    uint32_t numel = 0;
+    uint64_t out = 0;                 // element index in the output workspace
+    LaneSpec spec;
+    const Codebook* book = nullptr;   // nullptr: raw exponent lane
+    uint64_t bit_length = 0;
+    uint32_t n_windows = 0;
+    std::vector<uint8_t> bits;        // padded bitstream, or padded raw exponent lane
+    std::vector<uint16_t> meta;       // per window: gap | count << 8
+    std::vector<uint8_t> lanes;       // element_size - 1 raw lanes, lane_stride apart
+    uint32_t lane_stride = 0;
+    std::vector<nz_tile> tiles;       // frag field relative to this fragment (0)
+    uint32_t kind = NZ_KIND_RAW;
+
+    uint64_t bits_offset_size() const { return bits.size(); }
+    uint64_t meta_size() const { return meta.size() * 2; }
+};
+
+// Encodes the elements `src[0 .. numel * element_size)` of one chunk.
+// Mirrors encode_gpu_layout (gpu_layout.h:185-241): reorder, split lanes,
+// greedy pairs only when index + 1 < numel.
+Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const LaneSpec& spec,
+                         const Codebook* book);
+
+inline uint64_t align16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+
+// Bytes a fragment occupies in the packed buffer (bits, meta, lanes).
+uint64_t packed_size(const Fragment& f);
+
+// Writes the fragment at `dst + offset` (dst is the packed host buffer whose
+// byte 0 is device byte `base`) and fills its descriptor.
+void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lut_offset,
+                   nz_frag_desc* desc);
+
+// Splits `n_tiles` tiles into workgroup ranges that never mix fragments of
+// different LUTs or kinds.
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                               uint32_t target_groups);
+
+// CPU emulation of the decode kernel over a packed buffer; writes words
+// into `out` (the output workspace image).
+void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                    const nz_work* work, uint32_t n_work, unsigned element_size, bool reorder,
+                    uint8_t* out);
+
+}  // namespace nz

@@ -1,0 +1,79 @@
+// nz_format.h -- device layout shared by the host encoder and the gfx950
+// decode kernel.
+//
+// A *fragment* is one chunk of one tensor (the reference's GPUWeightGroup,
+// neuralzip/gpu/inference.py:143-168). Its selected byte lane (the exponent
+// lane) is either stored raw or as an MSB-first canonical-Huffman bitstream;
+// the other byte lanes are stored raw. Everything of a model lives in one
+// packed device buffer; descriptors hold byte offsets into it.
+//
+// Bitstream partition. Lane-sized *windows* of 64 bits: window w owns the
+// codes that the decoder starts at bit positions in [64w, 64w + 64). The
+// decoder consumes whole LUT steps (one to three tokens, or one long code),
+// so the first step of window w starts at 64w + gap[w], where gap[w] is the
+// overshoot of window w-1's last step; count[w] is the number of exponent
+// bytes that window w emits. Both come from a CPU simulation of the kernel's
+// own step sequence, which replaces the reference's count pass
+// (decode.cu:198-222) and its 4/8-bit restart gaps (gpu_layout.h:128-183).
+//
+// Tiles. A tile is up to 64 consecutive windows (one wavefront) whose counts
+// sum to at most NZ_TILE_OUT bytes; the wavefront turns counts into output
+// positions with a ballot prefix scan, stages the exponent bytes in LDS and
+// writes merged words with 16-byte stores.
+#pragma once
+#include <stdint.h>
+
+#define NZ_WINDOW_BITS 64
+#define NZ_WAVE 64
+#define NZ_TILE_OUT 2048          // max exponent bytes staged per tile
+#define NZ_RAW_TILE 2048          // elements per tile of a raw fragment
+#define NZ_LUT_BITS 12
+#define NZ_LUT_ENTRIES (1 << NZ_LUT_BITS)
+#define NZ_BITS_PAD 16            // zero bytes after each bitstream
+
+// LUT image (uint32 words), uploaded once per codebook:
+//   [0] number of escape lengths E   [1] number of escape tokens T
+//   [2] image size in words           [3] longest code length
+//   [4, 4 + 4096)  primary entries
+//   then E records of 6 words: limit(lo,hi) first(lo,hi) base length
+//   then T escape token entries
+// Primary entry: bytes b0 | b1 << 8 | b2 << 16, consumed bits << 24
+// (1..12; 0 marks an escape), byte count << 28 (1..3).
+// Escape token entry: bytes | byte count << 28.
+#define NZ_LUT_HEADER 4
+#define NZ_ESC_RECORD 6
+#define NZ_LUT_MAX_WORDS (NZ_LUT_HEADER + NZ_LUT_ENTRIES + NZ_ESC_RECORD * 56 + 512)
+
+enum nz_kind : uint32_t { NZ_KIND_RAW = 0, NZ_KIND_SHORT = 1, NZ_KIND_LONG = 2 };
+
+struct nz_frag_desc {            // 64 bytes
+    uint64_t bits;               // bitstream offset (raw exponent lane for raw fragments)
+    uint64_t meta;               // window metadata offset (uint16 gap | count << 8)
+    uint64_t lanes;              // raw lane 0 offset; lane k at lanes + k * lane_stride
+    uint64_t out;                // first element's index in the output workspace
+    uint64_t lut;                // LUT image offset (unused for raw fragments)
+    uint64_t bit_length;
+    uint32_t numel;
+    uint32_t lane_stride;
+    uint32_t kind;
+    uint32_t reserved;
+};
+
+struct nz_tile {                 // 16 bytes, one wavefront's work
+    uint32_t frag;
+    uint32_t win0;               // first window (Huffman fragments)
+    uint32_t out0;               // first element, relative to the fragment
+    uint16_t n_win;              // windows in the tile (Huffman fragments)
+    uint16_t n_out;              // elements in the tile
+};
+
+struct nz_work {                 // 16 bytes, one workgroup's contiguous tile range
+    uint32_t tile0, tile1;
+    uint32_t lut_frag;           // fragment whose LUT the workgroup stages
+    uint32_t kind;
+};
+
+// Raw lanes and raw exponent lanes are stored with `out % V` leading pad
+// bytes (V elements per 16-byte vector) so that a vector-aligned output
+// element maps to a vector-aligned lane address.
+static inline uint32_t nz_vector_elements(int element_size) { return 16u / (uint32_t)element_size; }

@@ -1,0 +1,59 @@
+"""Per-dtype byte-lane layout (neuralzip/dtypes.py:7-85).
+
+The selected lane is the exponent byte after moving the sign below the
+exponent (bfloat16, float32), or the raw high byte for float16.
+"""
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+@dataclass(frozen=True)
+class DTypeSpec:
+    name: str
+    torch_dtype: torch.dtype
+    numpy: np.dtype
+    element_size: int
+    bit_reorder: int
+    mantissa_bits: int
+    exponent_mask: int
+    exponent_stream: int | None = None
+    global_codebooks: tuple[tuple[int, str], ...] = ()
+
+    @property
+    def stream_ids(self):
+        return range(self.element_size)
+
+    @property
+    def selected_stream(self):
+        """The lane the codecs compress (neuralzip/compressor.py:61-64)."""
+        return self.exponent_stream if self.exponent_stream is not None else self.element_size - 1
+
+    def reorder_bytes(self, raw_bytes, *, restore=False):
+        """Move the sign below the exponent, or undo it; layout 0 is identity."""
+        if not self.bit_reorder:
+            return raw_bytes
+        unsigned = self.numpy.type
+        exponent_bits = self.exponent_mask.bit_length()
+        values = np.frombuffer(raw_bytes, dtype=self.numpy)
+        mantissa = values & unsigned((1 << self.mantissa_bits) - 1)
+        if restore:
+            sign = (values << unsigned(exponent_bits)) & unsigned(1 << (self.mantissa_bits + exponent_bits))
+            exponent = (values >> unsigned(1)) & unsigned(self.exponent_mask << self.mantissa_bits)
+        else:
+            sign = (values >> unsigned(exponent_bits)) & unsigned(1 << self.mantissa_bits)
+            exponent = (values << unsigned(1)) & unsigned(self.exponent_mask << (self.mantissa_bits + 1))
+        return (sign | exponent | mantissa).astype(self.numpy, copy=False).tobytes()
+
+    def extract_exponents(self, raw_bytes):
+        """Exponent fields of the original words."""
+        values = np.frombuffer(raw_bytes, dtype=self.numpy)
+        return (values >> self.mantissa_bits) & self.exponent_mask
+
+
+bfloat16 = DTypeSpec("bfloat16", torch.bfloat16, np.dtype("<u2"), 2, 1, 7, 0xFF, exponent_stream=1)
+float16 = DTypeSpec("float16", torch.float16, np.dtype("<u2"), 2, 0, 10, 0x1F)
+float32 = DTypeSpec("float32", torch.float32, np.dtype("<u4"), 4, 1, 23, 0xFF, exponent_stream=3)
+
+DTYPES = {spec.torch_dtype: spec for spec in (float16, bfloat16, float32)}

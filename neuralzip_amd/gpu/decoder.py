@@ -1,0 +1,161 @@
+"""HIP launcher for the exponent-lane decode kernel.
+
+Replaces the reference's CuPy/NVRTC launcher (neuralzip/gpu/decoder.py:28-215)
+with calls through the C ABI of libneuralzip_hip.so. Instead of five small
+device tensors per chunk (neuralzip/gpu/inference.py:401-432), every
+fragment of an export lives in one packed device buffer (DeviceStore); a
+PreparedBatch holds the tile and workgroup arrays of one launch.
+"""
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from neuralzip_amd import _native
+from neuralzip_amd._native import FRAG_DESC, KIND_LONG, KIND_RAW, TILE
+
+THREADS_PER_BLOCK = 256
+WINDOW_BITS = 64
+# Workgroups per launch the work planner aims at: several per CU on 256 CUs.
+TARGET_GROUPS = 2048
+
+
+def _align(value, alignment=256):
+    return (value + alignment - 1) // alignment * alignment
+
+
+class DeviceStore:
+    """LUT images and encoded fragments of one export, packed on a device.
+
+    `tensors` is a sequence of (layout, codebook_ids, workspace_offset) where
+    `layout` is a _native.Layout whose fragments were encoded with output
+    offsets relative to their tensor, `codebook_ids` names each fragment's
+    codebook (-1 for raw) and `workspace_offset` is the tensor's first
+    element in its workspace. `codebooks` maps ids to objects with `.lut()`.
+    """
+
+    def __init__(self, codebooks, tensors, device):
+        self.device = torch.device(device)
+        ids = sorted({i for _, ids, _ in tensors for i in ids if i != -1})
+        images = {i: codebooks[i].lut() for i in ids}
+        self.lut_offsets = {}
+        cursor = 0
+        for i in ids:
+            self.lut_offsets[i] = cursor
+            cursor += _align(images[i].nbytes, 16)
+        lut_bytes = _align(cursor)
+        tensor_offsets = []
+        cursor = lut_bytes
+        for layout, _, _ in tensors:
+            tensor_offsets.append(cursor)
+            cursor += _align(layout.packed_bytes)
+        self.nbytes = max(cursor, 256)
+        self.buffer = torch.empty(self.nbytes, dtype=torch.uint8, device=self.device)
+        staging = np.zeros(lut_bytes, dtype=np.uint8)
+        for i in ids:
+            off = self.lut_offsets[i]
+            staging[off:off + images[i].nbytes] = images[i].view(np.uint8)
+        if lut_bytes:
+            self.buffer[:lut_bytes].copy_(torch.from_numpy(staging))
+        descs, tiles, tile_starts = [], [], [0]
+        frag_base = 0
+        for (layout, cb_ids, workspace_offset), offset in zip(tensors, tensor_offsets):
+            if workspace_offset % 16:
+                raise ValueError("Workspace offsets must be multiples of 16 elements.")
+            host = np.zeros(_align(layout.packed_bytes), dtype=np.uint8)
+            luts = np.array([self.lut_offsets.get(i, 0) for i in cb_ids], dtype=np.uint64)
+            d, t = layout.pack(host, offset, luts, frag_base)
+            d["out"] += np.uint64(workspace_offset)
+            self.buffer[offset:offset + host.size].copy_(torch.from_numpy(host))
+            descs.append(d)
+            tiles.append(t)
+            counts = np.bincount(t["frag"] - frag_base, minlength=layout.n_fragments)
+            tile_starts.extend((tile_starts[-1] + np.cumsum(counts)).tolist())
+            frag_base += layout.n_fragments
+        self.descs = np.concatenate(descs) if descs else np.zeros(0, FRAG_DESC)
+        self.tiles = np.concatenate(tiles) if tiles else np.zeros(0, TILE)
+        self.tile_starts = np.asarray(tile_starts, dtype=np.int64)
+        self.frags = torch.from_numpy(self.descs.view(np.uint8).copy()).to(self.device)
+        self.frag_base = {}
+
+    def fragment_tiles(self, index):
+        return self.tiles[self.tile_starts[index]:self.tile_starts[index + 1]]
+
+
+@dataclass(frozen=True)
+class PreparedBatch:
+    """One launch: the workgroup plan over the tiles of some fragments."""
+    descriptor_tensors: tuple = field(repr=False)      # (tiles, work) on the device
+    device: torch.device
+    layout: tuple                                      # (element_size, bit_reorder, long_codes)
+    kernel_grid: tuple
+    store: DeviceStore = field(repr=False)
+    output: torch.Tensor = field(repr=False)
+    outputs: tuple = field(repr=False, default=())
+    algorithmic_bytes: int = 0
+
+
+def layout_key(desc, dtype):
+    return (dtype.element_size, bool(dtype.bit_reorder), int(desc["kind"]) == KIND_LONG)
+
+
+class HIPDecoder:
+    """prepare_group / prepare_batch / decode_batch, as CuPyDecoder offers."""
+
+    def prepare_group(self, device_index, group):
+        """Validates a group before any weight is removed (decoder.py:121-128)."""
+        dtype = group.encoded.dtype
+        if dtype.element_size == 2 and not dtype.bit_reorder and dtype.mantissa_bits != 10:
+            raise ValueError("Unsupported 16-bit layout for the GPU decoder.")
+        if dtype.element_size == 4 and not dtype.bit_reorder:
+            raise ValueError("Unsupported 32-bit layout for the GPU decoder.")
+        if dtype.bit_reorder and dtype.exponent_mask.bit_length() != 8:
+            raise ValueError("The GPU decoder needs a byte-aligned 8-bit exponent.")
+        _native.lib()
+        return group.layout
+
+    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), target_groups=TARGET_GROUPS):
+        """Tiles of `fragment_indices` (one dtype and kind) and their workgroup plan."""
+        fragment_indices = list(fragment_indices)
+        if not fragment_indices:
+            raise ValueError("A decode batch must contain at least one group.")
+        keys = {layout_key(store.descs[i], dtype) for i in fragment_indices if store.descs[i]["kind"] != KIND_RAW}
+        if len(keys) > 1:
+            raise ValueError("A decode batch must use one layout.")
+        key = keys.pop() if keys else (dtype.element_size, bool(dtype.bit_reorder), False)
+        tiles = np.concatenate([store.fragment_tiles(i) for i in fragment_indices])
+        work = _native.plan_work(store.descs, tiles, target_groups)
+        device = store.device
+        tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
+        work_t = torch.from_numpy(work.view(np.uint8).copy()).to(device)
+        return PreparedBatch((tiles_t, work_t), device, key, (len(work),), store, output, tuple(outputs),
+                             algorithmic_bytes(store.descs[fragment_indices], dtype))
+
+    def decode_batch(self, prepared, stream=None):
+        if stream is None:
+            stream = torch.cuda.current_stream(prepared.device)
+        tiles_t, work_t = prepared.descriptor_tensors
+        element_size, bit_reorder, long_codes = prepared.layout
+        _native.decode_launch(prepared.store.buffer.data_ptr(), prepared.store.frags.data_ptr(),
+                              tiles_t.data_ptr(), work_t.data_ptr(), prepared.kernel_grid[0], element_size,
+                              bit_reorder, long_codes, prepared.output.data_ptr(), stream.cuda_stream)
+        return prepared.outputs
+
+
+def algorithmic_bytes(descs, dtype):
+    """Bytes a decode must move: exponent bits (or raw exponent bytes), raw
+    lanes, window metadata and decoded words (LUT staging excluded)."""
+    numel = descs["numel"].astype(np.int64)
+    raw = descs["kind"] == KIND_RAW
+    bits = np.where(raw, numel, (descs["bit_length"].astype(np.int64) + 7) // 8)
+    windows = np.where(raw, 0, (descs["bit_length"].astype(np.int64) + WINDOW_BITS - 1) // WINDOW_BITS)
+    lanes = numel * (dtype.element_size - 1)
+    written = numel * dtype.element_size
+    return int(bits.sum() + 2 * windows.sum() + lanes.sum() + written.sum())
+
+
+_DECODER = HIPDecoder()
+
+
+def default_decoder():
+    return _DECODER

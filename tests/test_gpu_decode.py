@@ -1,0 +1,110 @@
+"""GPU parity of the gfx950 decode kernel through the C ABI.
+
+Every case compares the decoded workspace bit for bit with the original
+words and with the CPU emulation of the same launch; workspaces are poisoned
+with 0xA5 and decoded twice (_experiment_kernel_checks.py:59-121, 163-190).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from neuralzip_amd import _native
+from neuralzip_amd.dtypes import DTYPES
+from nz_helpers import Encoded, segment_lengths, segment_tensor, singleton_header
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, target_groups=2048):
+    device = torch.device("cuda:0")
+    work_all = _native.plan_work(descs, tiles, target_groups)
+    out = torch.full((workspace_elements * element_size + 64,), 0xA5, dtype=torch.uint8, device=device)
+    base_t = torch.from_numpy(base).to(device)
+    frags_t = torch.from_numpy(descs.view(np.uint8).copy()).to(device)
+    tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
+    stream = torch.cuda.current_stream(device)
+    for long_codes in (0, 1):
+        sel = [w for w in work_all if (w["kind"] == _native.KIND_LONG) == bool(long_codes)]
+        if not sel:
+            continue
+        work_t = torch.from_numpy(np.array(sel, dtype=_native.WORK).view(np.uint8).copy()).to(device)
+        _native.decode_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), work_t.data_ptr(),
+                              len(sel), element_size, bit_reorder, long_codes, out.data_ptr(),
+                              stream.cuda_stream)
+    torch.cuda.synchronize(device)
+    return out.cpu().numpy(), work_all
+
+
+def check_case(tensors, codebooks, dtype, repeats=2, target_groups=2048):
+    spec = DTYPES[dtype]
+    enc = Encoded(tensors, codebooks)
+    base, descs, tiles = enc.host_image()
+    size = max(off + raw.size // spec.element_size for raw, _, _, _, off in tensors)
+    for _ in range(repeats):
+        got, work = run_gpu(base, descs, tiles, spec.element_size, spec.bit_reorder, size, target_groups)
+        emu = np.full_like(got, 0xA5)
+        _native.emulate_decode(base, descs, tiles, work, spec.element_size, spec.bit_reorder, emu)
+        for raw, _, _, _, off in tensors:
+            lo = off * spec.element_size
+            assert np.array_equal(got[lo:lo + raw.size], raw)
+        assert np.array_equal(got, emu)
+
+
+def test_config1_shape_singleton_bf16():
+    g = torch.Generator().manual_seed(0)
+    raw = (torch.randn(4096, 4096, generator=g) * 0.02).bfloat16().view(torch.uint8).numpy().reshape(-1)
+    book = _native.Codebook(singleton_header(raw, torch.bfloat16))
+    ids = [0] * 128
+    check_case([(raw, torch.bfloat16, 131072, ids, 0)], {0: book}, torch.bfloat16, repeats=1)
+
+
+@pytest.mark.parametrize("max_bits", [12, 32, 33, 56])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_segment_boundaries(max_bits, dtype):
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(max_bits), vocab)
+    assert book.longest == max_bits
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
+    raw = segment_tensor(dtype, symbols)
+    check_case([(raw, dtype, 1 << 20, [0], 0)], {0: book}, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_raw_fragment_between_compressed_chunks_and_odd_offsets(dtype):
+    spec = DTYPES[dtype]
+    rng = np.random.default_rng(7)
+    t = (torch.from_numpy(rng.standard_normal(257 * 513).astype(np.float32)) * 0.02).to(dtype)
+    raw = t.view(torch.uint8).numpy().reshape(-1).copy()
+    header = singleton_header(raw, dtype)
+    book = _native.Codebook(header)
+    step = 4093                      # odd chunk size: misaligned fragment starts
+    n = -(-t.numel() // step)
+    ids = [0] * n
+    ids[n // 2] = -1
+    other = raw[: 3001 * spec.element_size].copy()
+    check_case([(raw, dtype, step, ids, 5), (other, dtype, 1000, [0, -1, 0, 0], 5 + t.numel() + 3)],
+               {0: book}, dtype)
+
+
+def test_long_codes_from_skewed_counts():
+    # _experiment_kernel_checks.py:214-259: counts[256] = 1 << 52 forces codes far beyond 12 bits
+    vocab = bytes((127, 127, 125, 126))
+    counts = [1 << (i // 8) for i in range(258)]
+    counts[256] = 1 << 52
+    header = oracle.build_mixed_codebook(counts, vocab)
+    book = _native.Codebook(header, vocab)
+    assert book.longest > 12
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [126], dtype=np.uint8)
+    raw = segment_tensor(torch.bfloat16, symbols)
+    check_case([(raw, torch.bfloat16, 1 << 20, [0], 0)], {0: book}, torch.bfloat16)
+
+
+@pytest.mark.parametrize("target_groups", [1, 7, 100000])
+def test_work_partitions_give_identical_output(target_groups):
+    g = torch.Generator().manual_seed(3)
+    raw = (torch.randn(1000, 1000, generator=g) * 0.05).bfloat16().view(torch.uint8).numpy().reshape(-1)
+    books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16)),
+             1: _native.Codebook(singleton_header(raw[: 20000], torch.bfloat16, prior=3))}
+    ids = [(0, 1, -1)[j % 3] for j in range(-(-1000000 // 65536))]
+    check_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, target_groups=target_groups)

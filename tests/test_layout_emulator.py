@@ -1,0 +1,111 @@
+"""The GPU layout and the kernel's algorithm, checked on the CPU.
+
+The emulator (nz_emulate_decode) performs the kernel's per-lane window
+decode, ballot-scan staging and vector assembly; these cases mirror
+tests/test_gpu_decode.py so that layout and indexing mistakes show up here
+before a GPU run.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from neuralzip_amd import _native
+from neuralzip_amd.dtypes import DTYPES
+from nz_helpers import Encoded, segment_lengths, segment_tensor, singleton_header
+
+
+def emulate_case(tensors, codebooks, dtype, target_groups=2048):
+    spec = DTYPES[dtype]
+    base, descs, tiles = Encoded(tensors, codebooks).host_image()
+    size = max(off + raw.size // spec.element_size for raw, _, _, _, off in tensors)
+    out = np.full(size * spec.element_size + 64, 0xA5, dtype=np.uint8)
+    work = _native.plan_work(descs, tiles, target_groups)
+    assert work["tile1"][-1] == len(tiles) and work["tile0"][0] == 0
+    assert np.all(work["tile0"][1:] == work["tile1"][:-1])
+    _native.emulate_decode(base, descs, tiles, work, spec.element_size, spec.bit_reorder, out)
+    for raw, _, _, _, off in tensors:
+        lo = off * spec.element_size
+        assert np.array_equal(out[lo:lo + raw.size], raw)
+    return descs, tiles
+
+
+@pytest.mark.parametrize("max_bits", [12, 32, 33, 56])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_segment_boundaries(max_bits, dtype):
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(max_bits), vocab)
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
+    descs, tiles = emulate_case([(segment_tensor(dtype, symbols), dtype, 1 << 20, [0], 0)], {0: book}, dtype)
+    assert descs["kind"][0] == (_native.KIND_LONG if max_bits > 32 else _native.KIND_SHORT)
+    # dense 1-bit pair codes: tiles shrink below 64 windows to respect staging
+    assert tiles["n_out"].max() <= 2048
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_raw_fragment_and_odd_offsets(dtype):
+    spec = DTYPES[dtype]
+    rng = np.random.default_rng(7)
+    t = (torch.from_numpy(rng.standard_normal(257 * 513).astype(np.float32)) * 0.02).to(dtype)
+    raw = t.view(torch.uint8).numpy().reshape(-1).copy()
+    book = _native.Codebook(singleton_header(raw, dtype))
+    n = -(-t.numel() // 4093)
+    ids = [0] * n
+    ids[n // 2] = -1
+    other = raw[: 3001 * spec.element_size].copy()
+    emulate_case([(raw, dtype, 4093, ids, 5), (other, dtype, 1000, [0, -1, 0, 0], 5 + t.numel() + 3)],
+                 {0: book}, dtype)
+
+
+def test_long_codes_from_skewed_counts():
+    vocab = bytes((127, 127, 125, 126))
+    counts = [1 << (i // 8) for i in range(258)]
+    counts[256] = 1 << 52
+    book = _native.Codebook(oracle.build_mixed_codebook(counts, vocab), vocab)
+    assert book.longest > 12
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [126], dtype=np.uint8)
+    emulate_case([(segment_tensor(torch.bfloat16, symbols), torch.bfloat16, 1 << 20, [0], 0)], {0: book},
+                 torch.bfloat16)
+
+
+@pytest.mark.parametrize("target_groups", [1, 7, 100000])
+def test_work_partitions(target_groups):
+    g = torch.Generator().manual_seed(3)
+    raw = (torch.randn(300, 1000, generator=g) * 0.05).bfloat16().view(torch.uint8).numpy().reshape(-1)
+    books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16)),
+             1: _native.Codebook(singleton_header(raw[:20000], torch.bfloat16, prior=3))}
+    ids = [(0, 1, -1)[j % 3] for j in range(-(-300000 // 65536))]
+    emulate_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, target_groups)
+
+
+def test_codebook_lengths_match_the_oracle_on_golden_headers():
+    import json
+    from pathlib import Path
+    from zstd_frames import literal_blocks
+    golden = Path(__file__).resolve().parent / "golden"
+    for vector in json.loads((golden / "huff0_vectors.json").read_text())["vectors"]:
+        for block in literal_blocks((golden / vector["file"]).read_bytes()):
+            if block["kind"] != "huffman":
+                continue
+            expected = oracle.Huff0Table.from_header(block["tree"]).codes()[0]
+            lengths, codes = _native.Codebook(block["tree"]).export()
+            assert np.array_equal(lengths, expected)
+            # canonical: shortest first, codes increase with (length, symbol)
+            order = sorted((int(l), s) for s, l in enumerate(lengths) if l)
+            assert [int(codes[s]) for _, s in order] == sorted(int(codes[s]) for _, s in order)
+
+
+def test_codebook_errors_match_reference_messages():
+    with pytest.raises(_native.NativeError, match="256 singletons"):
+        _native.Codebook(b"NZM1" + bytes([8] * 255))
+    with pytest.raises(_native.NativeError, match="Oversubscribed"):
+        _native.Codebook(b"NZM1" + bytes([7] * 256))
+    with pytest.raises(_native.NativeError, match="Incomplete"):
+        _native.Codebook(b"NZM1" + bytes([9] * 256))
+    with pytest.raises(_native.NativeError, match="Duplicate"):
+        _native.Codebook(b"NZM1" + bytes([8] * 256 + [9, 9]), bytes((1, 1, 1, 1)))
+    with pytest.raises(_native.NativeError, match="no codebook entry"):
+        header = oracle.Huff0Table.from_lengths(bytes([1, 2, 2] + [0] * 253)).header()
+        book = _native.Codebook(header)
+        raw = segment_tensor(torch.bfloat16, np.array([0, 1, 2, 3], dtype=np.uint8))
+        _native.Layout([(raw, book, 0, DTYPES[torch.bfloat16])])
