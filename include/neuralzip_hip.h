@@ -144,6 +144,82 @@ int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_t
                       const nz_work* work, uint32_t n_work, int element_size, int bit_reorder,
                       uint8_t* out);
 
+/* ---- storage format (host codecs) -------------------------------------- */
+
+/* Huff0 tree description for a 256-bin histogram plus `prior_count` per
+ * symbol, code lengths limited to max_bits (<= 12). With header == NULL only
+ * *header_size is set. Replaces: _huff0_cpp.build_codebook_from_counts
+ * (binding_helpers.h:250-324 -> codebooks.h:1-42). Byte equality with Zstd's
+ * table construction is not claimed; the description is format-valid. */
+int nz_huff0_build(const uint64_t* counts256, uint32_t prior_count, uint32_t max_bits,
+                   uint8_t* header, size_t capacity, size_t* header_size);
+
+/* Greedy pair/singleton token histogram of one chunk, added into counts
+ * (256 + vocab_size / 2 entries). Replaces: _huff0_cpp.count_mixed_tokens
+ * (mixed_huffman.h:96-115), called once per chunk. */
+int nz_count_mixed_tokens(const uint8_t* data, size_t size, const uint8_t* vocab,
+                          size_t vocab_size, uint64_t* counts);
+
+/* One storage block with the codebook: a Huff0 4-stream block or an NZM1
+ * frame; *size == 0 when it does not fit or a symbol has no code.
+ * Replaces: encode_huff0_block_into / encode_mixed_block_into
+ * (codebooks.h:114-142, mixed_huffman.h:127-178). */
+int nz_codebook_encode_block(const nz_codebook* codebook, const uint8_t* src, size_t n,
+                             uint8_t* dst, size_t capacity, size_t* size);
+/* Replaces: decode_huff0_block_into / decode_mixed_block_into
+ * (codebooks.h:191-207, mixed_huffman.h:180-240). */
+int nz_codebook_decode_block(const nz_codebook* codebook, const uint8_t* src, size_t size,
+                             uint8_t* dst, size_t n);
+
+typedef struct {
+    const uint8_t* raw;                 /* numel * element_size bytes           */
+    uint64_t numel;
+    uint32_t element_size, bit_reorder, mantissa_bits, exponent_bits;
+    uint32_t stream_id, reserved;
+    uint64_t chunk_size;                /* symbols per chunk                    */
+    const nz_codebook* const* chunk_books;  /* per chunk; NULL for raw          */
+    const int64_t* chunk_ids;           /* per chunk codebook id, -1 for raw    */
+    const int32_t* chunk_modes;         /* 0 raw, 1 shared_huff0, 2 mixed_huffman */
+} nz_storage_tensor;
+
+typedef struct {                        /* one (tensor, lane, chunk) record     */
+    int32_t mode;                       /* 0 raw, 1 shared_huff0, 2 mixed_huffman */
+    int32_t reserved;
+    int64_t codebook_id;                /* -1 for raw                           */
+    uint64_t symbols, offset, size;     /* span in the output blob              */
+} nz_storage_chunk;
+
+/* Direct storage encode: `out` receives prefix, raw lanes and the compacted
+ * selected-lane payloads; records get element_size * n_chunks entries per
+ * tensor (lane-major). Replaces: _huff0_cpp.compress_direct_storage
+ * (direct_storage.h:72-214). */
+int nz_storage_compress(const nz_storage_tensor* tensors, size_t count, const uint8_t* prefix,
+                        size_t prefix_size, uint64_t min_saving_bytes, int threads,
+                        double compression_threshold, uint8_t* out, size_t capacity,
+                        size_t* out_size, nz_storage_chunk* records);
+
+typedef struct {
+    int32_t mode;                       /* 0 raw, 1 shared_huff0, 2 mixed_huffman */
+    int32_t reserved;
+    const uint8_t* payload;
+    uint64_t payload_size;
+    uint64_t symbols;
+    const nz_codebook* codebook;        /* NULL for raw                         */
+} nz_storage_in;
+
+typedef struct {
+    uint32_t element_size, bit_reorder;
+    uint64_t numel;
+    const nz_storage_in* chunks;        /* element_size groups, concatenated    */
+    const uint64_t* group_sizes;
+    uint8_t* output;                    /* numel * element_size bytes           */
+} nz_storage_decode_tensor;
+
+/* CPU storage decode with one job per aligned chunk (<= 16 threads, one
+ * below 512 KiB). Replaces: _huff0_cpp.decompress_mixed_streams_many
+ * (decode_queue.h:1-113); used when loading storage checkpoints. */
+int nz_storage_decompress(const nz_storage_decode_tensor* tensors, size_t count, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,7 @@ FRAG_DESC = np.dtype([("bits", "<u8"), ("meta", "<u8"), ("lanes", "<u8"), ("out"
                       ("bit_length", "<u8"), ("numel", "<u4"), ("lane_stride", "<u4"), ("kind", "<u4"),
                       ("reserved", "<u4")])
 TILE = np.dtype([("frag", "<u4"), ("win0", "<u4"), ("out0", "<u4"), ("n_win", "<u2"), ("n_out", "<u2")])
+# (n_win, n_out) are the low and high halves of the little-endian `counts` word
 WORK = np.dtype([("tile0", "<u4"), ("tile1", "<u4"), ("lut_frag", "<u4"), ("kind", "<u4")])
 assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16
 

@@ -13,7 +13,7 @@ LIBRARY = HERE / "libneuralzip_hip.so"
 ARCH = os.environ.get("NZ_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HOST_SOURCES = ("codebook.cpp", "layout.cpp", "capi.cpp")
+HOST_SOURCES = ("codebook.cpp", "layout.cpp", "codec.cpp", "capi.cpp", "capi_storage.cpp")
 DEVICE_SOURCES = ("hip/decode_gfx950.hip",)
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", str(CSRC), "-I", str(ROOT / "include")]
 # packed FP32 instructions stay disabled on every HIP translation unit

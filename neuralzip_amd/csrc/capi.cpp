@@ -10,80 +10,30 @@
 #include <thread>
 #include <vector>
 
+#include "capi_internal.hpp"
 #include "codebook.hpp"
 #include "layout.hpp"
 #include "neuralzip_hip.h"
 #include "nz_format.h"
-
-struct nz_codebook {
-    nz::Codebook book;
-};
 
 struct nz_layout {
     std::vector<nz::Fragment> fragments;
 };
 
 namespace {
-
 thread_local std::string g_error;
+}
 
+namespace nz_capi {
 int set_error(int code, const char* message) {
     g_error = message;
     return code;
 }
+}  // namespace nz_capi
 
-template <typename F>
-int guarded(F&& body) {
-    try {
-        body();
-        return 0;
-    } catch (const nz::Error& e) {
-        return set_error(e.code, e.what());
-    } catch (const std::bad_alloc&) {
-        return set_error(nz::kOutOfMemory, "Out of host memory.");
-    } catch (const std::exception& e) {
-        return set_error(nz::kInvalidArgument, e.what());
-    } catch (...) {
-        return set_error(nz::kInvalidArgument, "Unknown native failure.");
-    }
-}
-
-// run_parallel_jobs (neuralzip/native/common.h:134-185): at most 16
-// workers, one when the input is small; the first error wins.
-template <typename Job>
-void parallel_for(size_t count, size_t total_bytes, int threads, Job&& job) {
-    unsigned hw = std::thread::hardware_concurrency();
-    int workers = threads > 0 ? threads : static_cast<int>(hw ? hw : 1);
-    workers = std::max(1, std::min<int>({workers, 16, static_cast<int>(std::max<size_t>(count, 1))}));
-    if (total_bytes < (512u << 10)) workers = 1;
-    std::vector<std::string> errors(count);
-    std::vector<int> codes(count, 0);
-    std::atomic<size_t> next{0};
-    auto worker = [&]() {
-        for (size_t i; (i = next.fetch_add(1)) < count;) {
-            try {
-                job(i);
-            } catch (const nz::Error& e) {
-                errors[i] = e.what();
-                codes[i] = e.code;
-            } catch (const std::exception& e) {
-                errors[i] = e.what();
-                codes[i] = nz::kInvalidArgument;
-            }
-        }
-    };
-    if (workers == 1) {
-        worker();
-    } else {
-        std::vector<std::thread> pool;
-        for (int w = 0; w < workers; ++w) pool.emplace_back(worker);
-        for (auto& t : pool) t.join();
-    }
-    for (size_t i = 0; i < count; ++i)
-        if (codes[i]) throw nz::Error(codes[i], errors[i]);
-}
-
-}  // namespace
+using nz_capi::guarded;
+using nz_capi::parallel_for;
+using nz_capi::set_error;
 
 extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* work,
                                     uint32_t n_work, int element_size, int bit_reorder, int long_codes,
@@ -101,6 +51,11 @@ int nz_codebook_create(const uint8_t* header, size_t header_size, const uint8_t*
         if (!out || (!header && header_size)) nz::fail(nz::kInvalidArgument, "Null codebook argument.");
         auto book = std::make_unique<nz_codebook>();
         book->book = nz::build_codebook(header, header_size, vocab, vocab_size);
+        if (!book->book.mixed) {
+            std::array<uint8_t, 256> lengths{};
+            std::copy(book->book.lengths.begin(), book->book.lengths.end(), lengths.begin());
+            book->huff = nz::huff0_tables(lengths);
+        }
         *out = book.release();
     });
 }

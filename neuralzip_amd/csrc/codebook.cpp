@@ -249,6 +249,9 @@ void build_lut(Codebook& book) {
     for (unsigned t : esc)
         if (esc_lengths.empty() || esc_lengths.back() != book.lengths[t]) esc_lengths.push_back(book.lengths[t]);
 
+    book.single.assign(NZ_LUT_ENTRIES, 0);
+    for (uint32_t y = 0; y < NZ_LUT_ENTRIES; ++y)
+        if (single[y] >= 0) book.single[y] = static_cast<uint32_t>(single[y]) | (uint32_t(book.lengths[single[y]]) << 16);
     auto& lut = book.lut;
     lut.assign(NZ_LUT_HEADER + NZ_LUT_ENTRIES + NZ_ESC_RECORD * esc_lengths.size() + esc.size(), 0);
     lut[0] = static_cast<uint32_t>(esc_lengths.size());
@@ -323,6 +326,15 @@ unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* b
     *bytes = te & 0xFFFFu;
     *count = te >> 28;
     return L;
+}
+
+unsigned token_step(const Codebook& book, uint64_t window, uint32_t* bytes, unsigned* count) {
+    const uint32_t e = book.single[static_cast<uint32_t>(window >> (64 - NZ_LUT_BITS))];
+    if (!e) return lut_step(book.lut, window, bytes, count);   // escapes are single tokens
+    const unsigned token = e & 0xFFFFu;
+    *bytes = book.token_bytes[token];
+    *count = Codebook::token_width(token);
+    return e >> 16;
 }
 
 Codebook build_codebook(const uint8_t* header, size_t header_size, const uint8_t* vocab,

@@ -38,6 +38,7 @@ struct Codebook {
     std::vector<uint16_t> pair_token;   // 65536 entries, 0 = not a pair
     unsigned longest = 0;
     std::vector<uint32_t> lut;          // device LUT image (nz_format.h)
+    std::vector<uint32_t> single;       // 12-bit prefix -> token | length << 16 (0: longer code)
     uint64_t vocab_bytes = 0;
 
     unsigned token_count() const { return static_cast<unsigned>(lengths.size()); }
@@ -59,5 +60,8 @@ std::array<uint8_t, 256> huff0_lengths(const uint8_t* header, size_t size, size_
 // LUT image exactly as the kernel does.
 unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* bytes,
                   unsigned* count);
+
+// Exactly one token at the head of the window (storage decoding counts tokens).
+unsigned token_step(const Codebook& book, uint64_t window, uint32_t* bytes, unsigned* count);
 
 }  // namespace nz

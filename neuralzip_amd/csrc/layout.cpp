@@ -79,7 +79,7 @@ Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const
         std::memcpy(f.bits.data() + pad, sym.data(), numel);
         for (uint32_t start = 0; start < numel;) {
             const uint32_t end = std::min<uint32_t>(numel, (start + pad) / NZ_RAW_TILE * NZ_RAW_TILE + NZ_RAW_TILE - pad);
-            f.tiles.push_back({0, 0, start, 0, static_cast<uint16_t>(end - start)});
+            f.tiles.push_back({0, 0, start, (end - start) << 16});
             start = end;
         }
         return f;
@@ -153,15 +153,16 @@ Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const
     }
     if (total < numel) fail(kCorruptStream, "Layout simulation emitted fewer bytes than elements.");
     // group windows into wavefront tiles
+    const uint64_t capacity = nz_tile_capacity(static_cast<int>(es));
     uint64_t out0 = 0;
     for (uint64_t w = 0; w < n_windows;) {
         uint64_t end = w, sum = 0;
-        while (end < n_windows && end - w < NZ_WAVE && sum + counts[end] <= NZ_TILE_OUT) sum += counts[end++];
+        while (end < n_windows && end - w < NZ_WAVE && sum + counts[end] <= capacity) sum += counts[end++];
         if (end == w) fail(kLayoutLimit, "A window exceeds the tile staging capacity.");
         const uint64_t n_out = std::min<uint64_t>(sum, numel - std::min<uint64_t>(out0, numel));
         if (n_out == 0) fail(kCorruptStream, "Empty tile in layout.");
         f.tiles.push_back({0, static_cast<uint32_t>(w), static_cast<uint32_t>(out0),
-                           static_cast<uint16_t>(end - w), static_cast<uint16_t>(n_out)});
+                           static_cast<uint32_t>((end - w) | (n_out << 16))});
         out0 += sum;
         w = end;
     }
@@ -233,7 +234,7 @@ uint32_t lane_bytes(const uint8_t* base, const nz_frag_desc& f, uint64_t g, unsi
 void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
                     const nz_work* work, uint32_t n_work, unsigned es, bool reorder, uint8_t* out) {
     const uint64_t V = nz_vector_elements(static_cast<int>(es));
-    std::vector<uint8_t> stage(NZ_TILE_OUT + 32);
+    std::vector<uint8_t> stage(nz_tile_capacity(static_cast<int>(es)) + 32);
     for (uint32_t wi = 0; wi < n_work; ++wi) {
         // the workgroup stages the LUT of work[wi].lut_frag
         const nz_frag_desc& lf = frags[work[wi].lut_frag];
@@ -245,7 +246,8 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
         for (uint32_t t = work[wi].tile0; t < work[wi].tile1; ++t) {
             const nz_tile& tile = tiles[t];
             const nz_frag_desc& f = frags[tile.frag];
-            const uint64_t A0 = f.out + tile.out0, A1 = A0 + tile.n_out;
+            const uint32_t n_win = nz_tile_windows(tile.counts);
+            const uint64_t A0 = f.out + tile.out0, A1 = A0 + nz_tile_elements(tile.counts);
             if (f.kind == NZ_KIND_RAW) {
                 for (uint64_t g = A0; g < A1; ++g) {
                     const uint8_t e = base[f.bits + (g - f.out / V * V)];
@@ -256,11 +258,11 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
             const bool longmode = f.kind == NZ_KIND_LONG;
             // wavefront exclusive scan of counts
             uint32_t offset[NZ_WAVE] = {0};
-            for (unsigned l = 1; l < tile.n_win; ++l)
+            for (unsigned l = 1; l < n_win; ++l)
                 offset[l] = offset[l - 1] + (base[f.meta + 2 * (tile.win0 + l - 1) + 1]);
             const uint64_t s0 = A0 - A0 / V * V;
             std::fill(stage.begin(), stage.end(), 0xA5);
-            for (unsigned l = 0; l < tile.n_win; ++l) {
+            for (unsigned l = 0; l < n_win; ++l) {
                 const uint64_t w = tile.win0 + l;
                 const unsigned gap = base[f.meta + 2 * w];
                 const uint8_t* src = base + f.bits + 8 * w;

@@ -23,9 +23,16 @@
 #pragma once
 #include <stdint.h>
 
+#if defined(__HIPCC__)
+#define NZ_HD __host__ __device__
+#else
+#define NZ_HD
+#endif
+
 #define NZ_WINDOW_BITS 64
 #define NZ_WAVE 64
-#define NZ_TILE_OUT 2048          // max exponent bytes staged per tile
+#define NZ_TILE_OUT 2048          // max exponent bytes staged per tile (16-bit words)
+#define NZ_TILE_OUT32 1024        // the same for 32-bit words
 #define NZ_RAW_TILE 2048          // elements per tile of a raw fragment
 #define NZ_LUT_BITS 12
 #define NZ_LUT_ENTRIES (1 << NZ_LUT_BITS)
@@ -63,9 +70,12 @@ struct nz_tile {                 // 16 bytes, one wavefront's work
     uint32_t frag;
     uint32_t win0;               // first window (Huffman fragments)
     uint32_t out0;               // first element, relative to the fragment
-    uint16_t n_win;              // windows in the tile (Huffman fragments)
-    uint16_t n_out;              // elements in the tile
+    uint32_t counts;             // windows (Huffman fragments) | elements << 16
 };
+
+NZ_HD static inline uint32_t nz_tile_windows(uint32_t counts) { return counts & 0xFFFFu; }
+NZ_HD static inline uint32_t nz_tile_elements(uint32_t counts) { return counts >> 16; }
+NZ_HD static inline uint32_t nz_tile_capacity(int element_size) { return element_size == 4 ? NZ_TILE_OUT32 : NZ_TILE_OUT; }
 
 struct nz_work {                 // 16 bytes, one workgroup's contiguous tile range
     uint32_t tile0, tile1;
@@ -76,4 +86,4 @@ struct nz_work {                 // 16 bytes, one workgroup's contiguous tile ra
 // Raw lanes and raw exponent lanes are stored with `out % V` leading pad
 // bytes (V elements per 16-byte vector) so that a vector-aligned output
 // element maps to a vector-aligned lane address.
-static inline uint32_t nz_vector_elements(int element_size) { return 16u / (uint32_t)element_size; }
+NZ_HD static inline uint32_t nz_vector_elements(int element_size) { return 16u / (uint32_t)element_size; }
