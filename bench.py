@@ -1,0 +1,216 @@
+"""Decode-throughput benchmark of the gfx950 exponent-lane decoder.
+
+Workload (one MI355X): eight bf16 tensors of Llama-3-8B layer shapes
+(276.8 M elements, 554 MB decoded), values N(0, std^2) with std cycling over
+{0.005, 0.01, 0.02, 0.05, 0.1} and 0.1 % of entries replaced by
+std * Student-t(3), seed 1; NeuralZipSetup(cluster_js_threshold=0.05) picks
+the cluster codebooks (NZM1 pair/singleton or Huff0). One step decodes every
+chunk of the set from HBM-resident compressed data into an HBM workspace.
+
+Prints one JSON line: value = decoded GB/s (bytes written / time), plus the
+roofline of the decode kernel (algorithmic bytes per launch / mean launch
+duration, timed with HIP events on the launch stream) and a CPU baseline
+(the oracle's threaded storage decode of the same tensors on this host).
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBPS = 8000.0
+SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
+          (4096, 14336)]
+STDS = [0.005, 0.01, 0.02, 0.05, 0.1]
+WORKLOAD = ("eight bf16 tensors [4096x4096, 4096x14336, 14336x4096, 1024x4096, 1024x4096, 4096x4096, "
+            "14336x4096, 4096x14336], N(0, std^2) with std cycling {0.005,0.01,0.02,0.05,0.1}, 0.1% "
+            "std*Student-t(3) outliers, seed 1, NeuralZipSetup(cluster_js_threshold=0.05), 256 KiB chunks")
+
+
+def log(message):
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def make_tensors(seed=1):
+    rng = np.random.default_rng(seed)
+    tensors = {}
+    for i, shape in enumerate(SHAPES):
+        std = STDS[i % len(STDS)]
+        values = rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+        mask = rng.random(shape, dtype=np.float32) < 0.001
+        values[mask] = (std * rng.standard_t(3, int(mask.sum()))).astype(np.float32)
+        tensors[f"layers.{i}.weight"] = torch.from_numpy(values).bfloat16()
+    return tensors
+
+
+def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
+    """Oracle storage decode (decode_queue.h semantics) of the same tensors."""
+    import oracle
+    from neuralzip_amd.compressor import NeuralZipCompressor
+    from neuralzip_amd.storage import unpack_storage
+    blob, metadata, _, _ = NeuralZipCompressor(setup).encode(tensors.items())
+    codebooks, payloads = unpack_storage(blob, metadata)
+    tables = {b.codebook_id: (oracle.MixedTable(bytes(b.codebook), bytes(b.vocab)) if b.mode == "mixed_huffman"
+                              else oracle.Huff0Table.from_header(bytes(b.codebook))) for b in codebooks}
+    specs = [(t.element_size, bool(t.bit_reorder), t.numel,
+              tuple(tuple((c.mode, bytes(c.payload), c.symbol_count, tables.get(c.codebook_id)) for c in g.chunks)
+                    for g in t.groups)) for t in payloads]
+    decoded = sum(t.numel * t.element_size for t in payloads)
+    times, start = [], time.perf_counter()
+    for rep in range(warmups + reps):
+        t0 = time.perf_counter()
+        out = oracle.decompress_many(specs, threads=threads)
+        dt = time.perf_counter() - t0
+        if rep >= warmups:
+            times.append(dt)
+        if time.perf_counter() - start > budget_s and len(times) >= 3:
+            break
+    for (name, t), data in zip(tensors.items(), out):
+        if bytes(data) != t.view(torch.uint8).numpy().tobytes():
+            raise RuntimeError(f"oracle decode of {name} is not bit-exact")
+    med = statistics.median(times)
+    return {"value": round(decoded / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full workload, {len(times)} timed decodes (median) after {warmups} warmups, "
+                      f"{decoded} bytes decoded each"}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--target-groups", type=int, default=None)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: decode needs no collective and this build runs on one device; "
+              "run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from neuralzip_amd.dtypes import DTYPES
+    from neuralzip_amd.gpu import decoder as gpu_decoder
+    from neuralzip_amd.gpu.inference import export_tensors_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    from neuralzip_amd._native import KIND_LONG
+
+    t0 = time.perf_counter()
+    tensors = make_tensors()
+    log(f"generated {len(tensors)} tensors in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    setup = NeuralZipSetup(cluster_js_threshold=0.05).build(tensors)
+    modes = [b.mode for b in setup.codebooks]
+    log(f"setup: {len(setup.codebooks)} codebooks ({modes.count('mixed_huffman')} mixed) "
+        f"in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    exported = export_tensors_for_gpu(tensors, setup)
+    log(f"export: {len(exported.groups)} fragments in {time.perf_counter() - t0:.1f}s")
+
+    device = torch.device("cuda:0")
+    spec = DTYPES[torch.bfloat16]
+    store_tensors, offsets, offset = [], {}, 0
+    for layout, ids, _, config, name in exported.tensors:
+        store_tensors.append((layout, ids, offset))
+        offsets[name] = offset
+        offset = (offset + tensors[name].numel() + 127) // 128 * 128
+    store = gpu_decoder.DeviceStore(exported.codebooks, store_tensors, device)
+    workspace = torch.empty(offset, dtype=torch.bfloat16, device=device)
+    decoder = gpu_decoder.default_decoder()
+    kinds = {}
+    for f in range(len(store.descs)):
+        kinds.setdefault(int(store.descs[f]["kind"]) == KIND_LONG, []).append(f)
+    target = args.target_groups or gpu_decoder.TARGET_GROUPS
+    batches = [decoder.prepare_batch(store, members, spec, workspace, target_groups=target)
+               for _, members in sorted(kinds.items())]
+    decoded_bytes = sum(int(d["numel"]) for d in store.descs) * spec.element_size
+    stream = torch.cuda.current_stream(device)
+
+    for _ in range(args.warmup):
+        for batch in batches:
+            decoder.decode_batch(batch, stream)
+    torch.cuda.synchronize(device)
+    # per-launch events on the launch stream
+    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in batches]
+              for _ in range(args.steps)]
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    begin.record(stream)
+    for step in range(args.steps):
+        for batch, (a, b) in zip(batches, events[step]):
+            a.record(stream)
+            decoder.decode_batch(batch, stream)
+            b.record(stream)
+    end.record(stream)
+    torch.cuda.synchronize(device)
+    total_ms = begin.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    launch_ms = [statistics.mean(events[s][k][0].elapsed_time(events[s][k][1]) for s in range(args.steps))
+                 for k in range(len(batches))]
+    dominant = max(range(len(batches)), key=lambda k: launch_ms[k])
+    achieved = batches[dominant].algorithmic_bytes / (launch_ms[dominant] * 1e-3) / 1e9
+
+    # bit-exactness of the final step
+    if set(offsets) != set(tensors):
+        raise RuntimeError("every tensor of the workload must be GPU-compressed")
+    for name, t in tensors.items():
+        off = offsets[name]
+        got = workspace[off:off + t.numel()].view(torch.uint8).cpu()
+        if not torch.equal(got, t.reshape(-1).view(torch.uint8)):
+            raise RuntimeError(f"GPU decode of {name} is not bit-exact")
+    log(f"bit-exact; {ms_per_step:.4f} ms/step, launches {[round(m, 4) for m in launch_ms]} ms")
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / "decode_traffic.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        threads = min(os.cpu_count() or 1, 16)
+        baseline = cpu_baseline(tensors, setup, threads)
+        log(f"cpu baseline {baseline['value']} GB/s on {threads} threads")
+
+    line = {
+        "metric": "decoded weight GB/s + % HBM roofline; tok/s 8B-shape bs=1 vs uncompressed bf16",
+        "value": round(decoded_bytes * args.steps / (total_ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic",
+        "config": {
+            "workload": WORKLOAD,
+            "elements": int(decoded_bytes // 2),
+            "decoded_bytes": int(decoded_bytes),
+            "codebooks": len(setup.codebooks),
+            "mixed_codebooks": modes.count("mixed_huffman"),
+            "launches_per_step": len(batches),
+            "workgroups": [b.kernel_grid[0] for b in batches],
+            "algorithmic_bytes_per_step": int(sum(b.algorithmic_bytes for b in batches)),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

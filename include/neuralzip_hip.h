@@ -154,6 +154,11 @@ int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_t
 int nz_huff0_build(const uint64_t* counts256, uint32_t prior_count, uint32_t max_bits,
                    uint8_t* header, size_t capacity, size_t* header_size);
 
+/* Huff0 tree description of given code lengths (a complete code, <= 12
+ * bits). Replaces building a GPUCodebook from lengths (gpu/inference.py:20-27). */
+int nz_huff0_header_from_lengths(const uint8_t* lengths256, uint8_t* header, size_t capacity,
+                                 size_t* header_size);
+
 /* Greedy pair/singleton token histogram of one chunk, added into counts
  * (256 + vocab_size / 2 entries). Replaces: _huff0_cpp.count_mixed_tokens
  * (mixed_huffman.h:96-115), called once per chunk. */

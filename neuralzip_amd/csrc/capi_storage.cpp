@@ -73,6 +73,21 @@ int nz_huff0_build(const uint64_t* counts, uint32_t prior_count, uint32_t max_bi
     });
 }
 
+int nz_huff0_header_from_lengths(const uint8_t* lengths256, uint8_t* header, size_t capacity, size_t* header_size) {
+    return nz_capi::guarded([&] {
+        if (!lengths256 || !header_size) nz::fail(nz::kInvalidArgument, "Null Huff0 header argument.");
+        std::array<uint8_t, 256> lengths{};
+        std::copy(lengths256, lengths256 + 256, lengths.begin());
+        for (uint8_t l : lengths) if (l > 12) nz::fail(nz::kInvalidCodebook, "Huff0 codes are at most 12 bits.");
+        const auto bytes = nz::huff0_header_from_lengths(lengths);
+        *header_size = bytes.size();
+        if (header) {
+            if (capacity < bytes.size()) nz::fail(nz::kInvalidArgument, "Header buffer is too small.");
+            std::memcpy(header, bytes.data(), bytes.size());
+        }
+    });
+}
+
 int nz_count_mixed_tokens(const uint8_t* data, size_t size, const uint8_t* vocab, size_t vocab_size,
                           uint64_t* counts) {
     return nz_capi::guarded([&] {

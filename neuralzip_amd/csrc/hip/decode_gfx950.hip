@@ -31,7 +31,7 @@ constexpr int kWaves = kThreads / NZ_WAVE;
 
 // Minimum wavefronts per SIMD the register allocator must allow.
 #ifndef NZ_WAVES_PER_EU
-#define NZ_WAVES_PER_EU 5
+#define NZ_WAVES_PER_EU 6
 #endif
 
 __device__ __forceinline__ uint32_t bswap32(uint32_t x) { return __builtin_amdgcn_perm(0u, x, 0x00010203u); }

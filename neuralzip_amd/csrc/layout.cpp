@@ -152,12 +152,16 @@ Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const
         total += count;
     }
     if (total < numel) fail(kCorruptStream, "Layout simulation emitted fewer bytes than elements.");
-    // group windows into wavefront tiles
+    // Group windows into wavefront tiles. Only trailing windows can be empty:
+    // the previous window's last step may overrun the final code into the
+    // zero padding, past the start of the last window's range.
+    uint64_t used_windows = n_windows;
+    while (used_windows > 0 && counts[used_windows - 1] == 0) --used_windows;
     const uint64_t capacity = nz_tile_capacity(static_cast<int>(es));
     uint64_t out0 = 0;
-    for (uint64_t w = 0; w < n_windows;) {
+    for (uint64_t w = 0; w < used_windows;) {
         uint64_t end = w, sum = 0;
-        while (end < n_windows && end - w < NZ_WAVE && sum + counts[end] <= capacity) sum += counts[end++];
+        while (end < used_windows && end - w < NZ_WAVE && sum + counts[end] <= capacity) sum += counts[end++];
         if (end == w) fail(kLayoutLimit, "A window exceeds the tile staging capacity.");
         const uint64_t n_out = std::min<uint64_t>(sum, numel - std::min<uint64_t>(out0, numel));
         if (n_out == 0) fail(kCorruptStream, "Empty tile in layout.");

@@ -1,0 +1,482 @@
+"""GPU export and the on-the-fly decode runtime (neuralzip/gpu/inference.py).
+
+Export (once): choose hook blocks and Linear/Conv weights, give every chunk
+its codebook from the setup's transfer plan, and encode all chunks of a
+tensor into the wave64 GPU layout in one multi-threaded native call.
+
+Runtime (every forward): a forward pre-hook per block launches the gfx950
+decode of that block's weights into a workspace whose views are the
+modules' `weight` attributes. With prefetch enabled, the hook of block N
+also launches the decode of block N+1 on a side stream into the other
+workspace slot, ordered after everything already queued on the compute
+stream (which includes the last reads of that slot, by block N-1).
+"""
+from collections import defaultdict
+from dataclasses import dataclass, field
+from functools import partial
+
+import numpy as np
+import torch
+from torch import nn
+from transformers.pytorch_utils import Conv1D
+
+from neuralzip_amd import _native, huff0
+from neuralzip_amd._native import KIND_LONG, KIND_RAW
+from neuralzip_amd.compressor import NeuralZipCompressor
+from neuralzip_amd.dtypes import DTYPES, DTypeSpec
+from neuralzip_amd.gpu import decoder as gpu_decoder
+from neuralzip_amd.utils import _stream_chunk_size
+
+RUNTIME_ATTRIBUTE = "neuralzip_runtime"
+_GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
+# Tensor offsets in a workspace: 128 elements keeps views 256-byte aligned
+# and fragment starts 16-element aligned (the layout's vector alignment).
+WORKSPACE_ALIGNMENT = 128
+
+
+@dataclass(frozen=True, eq=False)
+class GPUCodebook:
+    """Code table of one codebook (inference.py:20-75).
+
+    Built from code lengths (values are kept for reference; the GPU layout
+    uses its own canonical codes) or, with `header`, from a payload header.
+    `decode_lut` is the device LUT image and `max_bits` the primary index
+    width of the reference (min(12, longest)).
+    """
+    code_lengths: tuple
+    code_values: tuple
+    vocab: bytes = b""
+    header: bytes = field(default=b"", repr=False)
+    max_bits: int = field(init=False)
+    longest: int = field(init=False)
+    native: object = field(init=False, repr=False)
+
+    def __post_init__(self):
+        longest = max(self.code_lengths, default=0)
+        if longest > (56 if self.vocab else 12):
+            raise ValueError("The GPU codebook exceeds its decoder's code-length limit.")
+        object.__setattr__(self, "longest", longest)
+        object.__setattr__(self, "max_bits", min(12, longest))
+        if not longest:
+            object.__setattr__(self, "native", None)
+            return
+        if len(self.code_lengths) != 256 + len(self.vocab) // 2:
+            raise ValueError("The GPU alphabet does not match its pair vocabulary.")
+        header = self.header or (b"NZM1" + bytes(self.code_lengths) if self.vocab
+                                 else huff0.huff0_header_from_lengths(self.code_lengths))
+        object.__setattr__(self, "native", _native.Codebook(header, self.vocab))
+
+    @classmethod
+    def from_payload(cls, payload):
+        lengths, values, _ = huff0.export_code_table(payload.codebook, max_bits=56, vocab=payload.vocab)
+        return cls(tuple(lengths), values, bytes(payload.vocab), header=bytes(payload.codebook))
+
+    @property
+    def decode_lut(self):
+        return () if self.native is None else self.native.lut()
+
+    def lut(self):
+        return self.native.lut()
+
+
+@dataclass(frozen=True, eq=False)
+class GPUEncodedSymbols:
+    """The coded selected lane of one fragment (inference.py:78-90): the
+    bitstream plus window metadata and tiles instead of restart gaps and
+    block output positions."""
+    layout: object = field(repr=False)
+    index: int
+    bit_length: int
+    symbol_count: int
+    bits_bytes: int
+    meta_bytes: int
+    n_tiles: int
+    kind: int
+
+    @property
+    def compressed_bytes(self):
+        tile_bytes = 16 * self.n_tiles
+        return self.bits_bytes + self.meta_bytes + tile_bytes
+
+
+@dataclass(frozen=True, eq=False)
+class GPUEncoded:
+    """One fragment: dtype, element count and per-lane streams (inference.py:93-108).
+
+    streams[k] is the GPUEncodedSymbols of the selected lane or the byte
+    count of a raw lane (raw lanes live only in the packed buffer)."""
+    dtype: DTypeSpec
+    numel: int
+    streams: tuple
+
+    @property
+    def raw_bytes(self):
+        return self.numel * self.dtype.element_size
+
+    @property
+    def compressed_bytes(self):
+        return sum(s if isinstance(s, int) else s.compressed_bytes for s in self.streams)
+
+
+def _fragment(layout, index, dtype, numel):
+    info = layout.info(index)
+    stream_id = dtype.selected_stream
+    if info["kind"] == KIND_RAW:
+        symbols = numel
+    else:
+        symbols = GPUEncodedSymbols(layout, index, info["bit_length"], numel, info["bits_bytes"],
+                                    info["meta_bytes"], info["n_tiles"], info["kind"])
+    streams = tuple(symbols if lane == stream_id else numel for lane in range(dtype.element_size))
+    return GPUEncoded(dtype, numel, streams)
+
+
+def encode_gpu_native(raw, codebook_header, *, dtype, stream_id, vocab=b"", codebook_handle=None):
+    """Encode one chunk (inference.py:111-131); the selected lane must be the
+    dtype's (the exponent byte, or the high byte of float16)."""
+    if stream_id != dtype.selected_stream:
+        raise ValueError("The GPU layout codes the dtype's selected byte lane.")
+    book = codebook_handle.handle if codebook_handle is not None else _native.Codebook(bytes(codebook_header),
+                                                                                        bytes(vocab))
+    data = np.frombuffer(bytes(raw), dtype=np.uint8)
+    layout = _native.Layout([(data, book, 0, dtype)])
+    return _fragment(layout, 0, dtype, data.size // dtype.element_size)
+
+
+@dataclass(frozen=True)
+class LinearWeightBinding:
+    module_name: str
+    tensor_name: str
+    shape: tuple
+    numel: int
+    workspace_offset: int
+
+
+@dataclass(frozen=True, eq=False)
+class GPUWeightGroup:
+    """One chunk of one weight (inference.py:143-168)."""
+    block_name: str
+    codebook_id: int
+    codebook: GPUCodebook
+    encoded: GPUEncoded
+    bindings: tuple
+    workspace_offset: int
+
+    @property
+    def layout(self):
+        dtype = self.encoded.dtype
+        symbols = self.encoded.streams[dtype.selected_stream]
+        long_codes = not isinstance(symbols, int) and symbols.kind == KIND_LONG
+        return (dtype.element_size, bool(dtype.bit_reorder), dtype.mantissa_bits, dtype.exponent_mask.bit_length(),
+                dtype.selected_stream, bool(self.codebook.vocab), long_codes)
+
+
+@dataclass(frozen=True, eq=False)
+class NeuralZipModelExport:
+    groups: tuple
+    tensors: tuple = field(default=(), repr=False)   # (layout, codebook ids, offset, dtype, block name)
+    codebooks: dict = field(default_factory=dict, repr=False)
+
+    @property
+    def block_order(self):
+        return tuple(dict.fromkeys(group.block_name for group in self.groups))
+
+    @property
+    def bindings(self):
+        return tuple(dict.fromkeys(binding for group in self.groups for binding in group.bindings))
+
+    @property
+    def workspace_sizes(self):
+        sizes = {}
+        for group in self.groups:
+            dtype = group.encoded.dtype.torch_dtype
+            sizes[dtype] = max(sizes.get(dtype, 0), group.workspace_offset + group.encoded.numel)
+        return sizes
+
+
+@dataclass(frozen=True)
+class _Candidate:
+    block_name: str
+    module_name: str
+    tensor_name: str
+    parameter: nn.Parameter = field(repr=False, compare=False)
+
+
+def _join(parent, child):
+    return f"{parent}.{child}" if parent and child else parent or child
+
+
+def _decode_hook_module(model, block_name):
+    parent_name, _, child_name = block_name.rpartition(".")
+    parent = model.get_submodule(parent_name)
+    # MultiheadAttention reads out_proj.weight without calling the child Linear
+    if child_name == "out_proj" and isinstance(parent, nn.MultiheadAttention):
+        return parent
+    return model.get_submodule(block_name)
+
+
+def _gpu_candidates(model):
+    """Blocks are ModuleList children (outermost that still owns Linear
+    layers of its own); other weight modules are their own blocks
+    (inference.py:232-274)."""
+    possible = [(_join(parent_name, child_name), child)
+                for parent_name, parent in model.named_modules(remove_duplicate=False)
+                if isinstance(parent, nn.ModuleList)
+                for child_name, child in parent._modules.items() if child is not None]
+    names = {name for name, _ in possible}
+    blocks = []
+    for name, module in possible:
+        if any(name.startswith(parent + ".") for parent, _ in blocks):
+            continue
+        nested = tuple(child + "." for child in names if child.startswith(name + "."))
+        if nested and all((_join(name, child) + ".").startswith(nested)
+                          for child, layer in module.named_modules(remove_duplicate=False)
+                          if isinstance(layer, nn.Linear)):
+            continue
+        blocks.append((name, module))
+    candidates = []
+    for module_name, module in model.named_modules(remove_duplicate=False):
+        if not isinstance(module, _GPU_WEIGHT_TYPES):
+            continue
+        parameter = module._parameters.get("weight")
+        if isinstance(parameter, nn.Parameter):
+            block = next((name for name, _ in blocks
+                          if module_name == name or module_name.startswith(name + ".")), module_name)
+            candidates.append(_Candidate(block, module_name, _join(module_name, "weight"), parameter))
+    return tuple(dict.fromkeys(c.block_name for c in candidates)), tuple(candidates)
+
+
+def _unique_candidates(model, candidates):
+    """Drop tied/shared parameters (inference.py:277-285)."""
+    occurrences = defaultdict(int)
+    for _name, parameter in model.named_parameters(remove_duplicate=False):
+        occurrences[id(parameter)] += 1
+    return tuple(c for c in candidates if c.parameter.numel() and occurrences[id(c.parameter)] == 1)
+
+
+def _align(value, alignment=WORKSPACE_ALIGNMENT):
+    return (value + alignment - 1) // alignment * alignment
+
+
+def _assemble_export(block_order, candidates, compressor, threads=0):
+    """Encode every candidate's chunks; keep a tensor only if its fragments
+    are smaller than its raw bytes (inference.py:288-336)."""
+    payloads = {int(p.codebook_id): p for p in compressor.export_codebooks()}
+    codebooks = {}
+    block_index = {name: i for i, name in enumerate(block_order)}
+    offsets = defaultdict(int)
+    groups, tensors = [], []
+    for member in sorted(candidates, key=lambda c: (block_index[c.block_name], c.module_name)):
+        parameter = member.parameter
+        config = DTYPES[parameter.dtype]
+        stream_id = config.selected_stream
+        modes = compressor._transfer_chunk_modes[compressor._transfer_plan_key(member.tensor_name, parameter,
+                                                                               stream_id)]
+        step = _stream_chunk_size(compressor.chunk_size, config.element_size)
+        raw = parameter.detach().cpu().contiguous().reshape(-1).view(torch.uint8).numpy()
+        ids, fragments = [], []
+        for chunk, mode in enumerate(modes):
+            codebook_id = int(mode.get("codebook_id", -1)) if mode["kind"] != "raw" else -1
+            if codebook_id != -1 and codebook_id not in codebooks:
+                codebooks[codebook_id] = GPUCodebook.from_payload(payloads[codebook_id])
+            start = chunk * step
+            part = raw[start * config.element_size:(start + step) * config.element_size]
+            book = codebooks[codebook_id].native if codebook_id != -1 else None
+            fragments.append((part, book, start, config))
+            ids.append(codebook_id)
+        layout = _native.Layout(fragments, threads=threads)
+        encoded = [_fragment(layout, i, config, len(f[0]) // config.element_size) for i, f in enumerate(fragments)]
+        if sum(e.compressed_bytes for e in encoded) >= raw.size:
+            continue
+        key = (member.block_name, parameter.dtype)
+        workspace_offset = offsets[key]
+        binding = LinearWeightBinding(member.module_name, member.tensor_name, tuple(parameter.shape),
+                                      parameter.numel(), workspace_offset)
+        for chunk, (codebook_id, enc) in enumerate(zip(ids, encoded)):
+            groups.append(GPUWeightGroup(member.block_name, codebook_id,
+                                         codebooks[codebook_id] if codebook_id != -1 else GPUCodebook((), ()),
+                                         enc, (binding,), workspace_offset + chunk * step))
+        tensors.append((layout, tuple(ids), workspace_offset, config, member.block_name))
+        offsets[key] = _align(workspace_offset + parameter.numel())
+    return NeuralZipModelExport(tuple(groups), tuple(tensors), codebooks)
+
+
+def export_model_for_gpu(model, setup, *, allowed_dtypes=DTYPES, threads=0):
+    """Export the frozen chunk tables, including adaptive singleton/pair codes."""
+    blocks, candidates = _gpu_candidates(model)
+    candidates = tuple(c for c in _unique_candidates(model, candidates)
+                       if c.parameter.dtype in DTYPES and c.parameter.dtype in allowed_dtypes
+                       and c.parameter.is_contiguous())
+    if not candidates:
+        return NeuralZipModelExport(())
+    compressor = NeuralZipCompressor(setup, gpu=True)
+    compressor.prepare_gpu_transfer_target(tuple((c.tensor_name, c.parameter) for c in candidates))
+    return _assemble_export(blocks, candidates, compressor, threads=threads)
+
+
+def export_tensors_for_gpu(named_tensors, setup, *, threads=0):
+    """Export a {name: tensor} set as one block per tensor (no model needed)."""
+    compressor = NeuralZipCompressor(setup, gpu=True)
+    named_tensors = tuple(named_tensors.items() if hasattr(named_tensors, "items") else named_tensors)
+    compressor.prepare_gpu_transfer_target(named_tensors)
+    candidates = tuple(_Candidate(name, name.rpartition(".")[0] or name, name, nn.Parameter(t, requires_grad=False))
+                       for name, t in named_tensors)
+    return _assemble_export(tuple(name for name, _ in named_tensors), candidates, compressor, threads=threads)
+
+
+def _binding_module(model, binding):
+    module = model.get_submodule(binding.module_name)
+    if not isinstance(module, _GPU_WEIGHT_TYPES):
+        raise TypeError(f"{binding.module_name!r} is not a supported weight module.")
+    return module
+
+
+class NeuralZipRuntime:
+    """Runtime attached to one model on one device (inference.py:379-509).
+
+    `workspaces[dtype]` holds every slot; a block's weights are views into
+    its slot. With `prefetch`, consecutive blocks use different slots and
+    block N+1 is decoded on `side_stream` while block N computes.
+    """
+
+    def __init__(self, model, exported, device, *, prefetch=True):
+        self.model = model
+        self.export = exported
+        self.device = torch.device(device)
+        self.prefetch = bool(prefetch)
+        self._decoder = gpu_decoder.default_decoder()
+        self._hook_handles = []
+        order = exported.block_order
+        n_slots = 1 if not self.prefetch or len(order) < 2 else (2 if len(order) % 2 == 0 else 3)
+        self.block_slot = {name: (i % 2 if n_slots > 1 else 0) for i, name in enumerate(order)}
+        if n_slots == 3:
+            self.block_slot[order[-1]] = 2
+        block_sizes = defaultdict(int)
+        for group in exported.groups:
+            key = (group.encoded.dtype.torch_dtype, self.block_slot[group.block_name])
+            block_sizes[key] = max(block_sizes[key], _align(group.workspace_offset + group.encoded.numel))
+        self.slot_offsets, self.workspaces = {}, {}
+        for dtype in {d for d, _ in block_sizes}:
+            cursor = 0
+            for slot in range(n_slots):
+                self.slot_offsets[(dtype, slot)] = cursor
+                cursor += _align(block_sizes.get((dtype, slot), 0))
+            self.workspaces[dtype] = torch.empty(max(cursor, 1), dtype=dtype, device=self.device)
+        # the packed device store: every tensor at its slot's offset
+        tensors, by_block, frag_base = [], defaultdict(list), 0
+        for layout, ids, offset, config, name in exported.tensors:
+            slot_base = self.slot_offsets[(config.torch_dtype, self.block_slot[name])]
+            tensors.append((layout, ids, slot_base + offset))
+            by_block[(name, config.torch_dtype)].extend(range(frag_base, frag_base + layout.n_fragments))
+            frag_base += layout.n_fragments
+        self.store = gpu_decoder.DeviceStore(exported.codebooks, tensors, self.device)
+        self._prepared_batches = defaultdict(list)
+        self.algorithmic_bytes = {}
+        for (name, dtype), frags in by_block.items():
+            spec = DTYPES[dtype]
+            kinds = defaultdict(list)
+            for f in frags:
+                kinds[int(self.store.descs[f]["kind"]) == KIND_LONG].append(f)
+            for long_codes, members in sorted(kinds.items()):
+                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype])
+                self._prepared_batches[name].append(batch)
+                self.algorithmic_bytes[name] = self.algorithmic_bytes.get(name, 0) + batch.algorithmic_bytes
+        self._groups_by_block = defaultdict(list)
+        for group in exported.groups:
+            self._groups_by_block[group.block_name].append(group)
+        self.side_stream = torch.cuda.Stream(self.device) if self.prefetch else None
+        self._pending = None   # (block name, event) decoded ahead on the side stream
+        torch.cuda.synchronize(self.device)
+
+    @classmethod
+    def attach(cls, model, exported, *, device=None, prefetch=True):
+        if hasattr(model, RUNTIME_ATTRIBUTE):
+            raise RuntimeError("This model already has a NeuralZip runtime.")
+        if not exported.groups:
+            raise ValueError("The setup produced no GPU-compressible weights.")
+        if device is None:
+            current = next(model.parameters()).device
+            device = current if current.type == "cuda" else "cuda"
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise ValueError("NeuralZip GPU inference requires a CUDA (HIP) device.")
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        decoder = gpu_decoder.default_decoder()
+        for group in exported.groups:
+            decoder.prepare_group(device.index, group)
+        for binding in exported.bindings:
+            module = _binding_module(model, binding)
+            module._parameters.pop("weight", None)
+            module.__dict__.pop("weight", None)
+        model.to(device).eval()
+        runtime = cls(model, exported, device, prefetch=prefetch)
+        runtime._install()
+        return runtime
+
+    def _binding_view(self, dtype, block_name, binding):
+        base = self.slot_offsets[(dtype, self.block_slot[block_name])] + binding.workspace_offset
+        return self.workspaces[dtype][base:base + binding.numel].view(binding.shape)
+
+    def _install(self):
+        for name, groups in self._groups_by_block.items():
+            for group in groups:
+                for binding in group.bindings:
+                    _binding_module(self.model, binding).__dict__["weight"] = self._binding_view(
+                        group.encoded.dtype.torch_dtype, name, binding)
+        for name in self.export.block_order:
+            handle = _decode_hook_module(self.model, name).register_forward_pre_hook(
+                partial(self._decode_block, name), prepend=True)
+            self._hook_handles.append(handle)
+        setattr(self.model, RUNTIME_ATTRIBUTE, self)
+
+    def _launch(self, block_name, stream):
+        for prepared in self._prepared_batches[block_name]:
+            self._decoder.decode_batch(prepared, stream)
+
+    def _decode_block(self, block_name, _module=None, _args=None):
+        current = torch.cuda.current_stream(self.device)
+        pending, self._pending = self._pending, None
+        if pending is not None and pending[0] == block_name:
+            current.wait_event(pending[1])
+        else:
+            if pending is not None:
+                current.wait_event(pending[1])   # the side stream must not still write a slot
+            self._launch(block_name, current)
+        if self.side_stream is None:
+            return
+        order = self.export.block_order
+        following = order[(order.index(block_name) + 1) % len(order)]
+        if following == block_name:
+            return
+        # everything queued so far (the last readers of `following`'s slot
+        # included) completes before the side stream overwrites that slot
+        ready = torch.cuda.Event()
+        ready.record(current)
+        self.side_stream.wait_event(ready)
+        self._launch(following, self.side_stream)
+        done = torch.cuda.Event()
+        done.record(self.side_stream)
+        self._pending = (following, done)
+
+    def drain(self):
+        """Order the compute stream after any pending side-stream decode."""
+        if self._pending is not None:
+            torch.cuda.current_stream(self.device).wait_event(self._pending[1])
+            self._pending = None
+
+    @torch.no_grad()
+    def materialized_weights(self):
+        """Yield compressed weights as bit-exact CPU tensors, one block at a time."""
+        self.drain()
+        yielded = set()
+        current = torch.cuda.current_stream(self.device)
+        for name in self.export.block_order:
+            self._launch(name, current)
+            torch.cuda.synchronize(self.device)
+            for group in self._groups_by_block[name]:
+                for binding in group.bindings:
+                    if binding.tensor_name in yielded:
+                        continue
+                    yielded.add(binding.tensor_name)
+                    view = self._binding_view(group.encoded.dtype.torch_dtype, name, binding)
+                    yield binding.tensor_name, view.detach().to("cpu", copy=True)

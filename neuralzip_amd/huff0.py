@@ -53,6 +53,7 @@ def _lib():
         vp, sz, u32, u64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64
         L.nz_huff0_build.argtypes = [vp, u32, u32, vp, sz, ctypes.POINTER(sz)]
         L.nz_count_mixed_tokens.argtypes = [vp, sz, vp, sz, vp]
+        L.nz_huff0_header_from_lengths.argtypes = [vp, vp, sz, ctypes.POINTER(sz)]
         L.nz_codebook_encode_block.argtypes = [vp, vp, sz, vp, sz, ctypes.POINTER(sz)]
         L.nz_codebook_decode_block.argtypes = [vp, vp, sz, vp, sz]
         L.nz_storage_compress.argtypes = [vp, sz, vp, sz, u64, ctypes.c_int, ctypes.c_double, vp, sz,
@@ -117,6 +118,18 @@ def build_codebook_from_counts(symbol_counts, *, prior_count=0, max_bits=11):
     _native.check(L.nz_huff0_build(counts.ctypes.data, int(prior_count), int(max_bits), header.ctypes.data,
                                    header.size, ctypes.byref(size)))
     return build_codebook_from_header(header.tobytes())
+
+
+def huff0_header_from_lengths(lengths):
+    """Tree description of a complete singleton code given by its lengths."""
+    arr = np.zeros(256, dtype=np.uint8)
+    arr[:len(lengths)] = np.asarray(lengths, dtype=np.uint8)
+    size = ctypes.c_size_t()
+    L = _lib()
+    _native.check(L.nz_huff0_header_from_lengths(arr.ctypes.data, None, 0, ctypes.byref(size)))
+    out = np.zeros(size.value, dtype=np.uint8)
+    _native.check(L.nz_huff0_header_from_lengths(arr.ctypes.data, out.ctypes.data, out.size, ctypes.byref(size)))
+    return out.tobytes()
 
 
 def build_codebook_from_header(codebook, *, vocab=b""):

@@ -116,8 +116,8 @@ class MixedTable:
         self._handle = handle
 
     def __del__(self):
-        if getattr(self, "_handle", None):
-            lib().nzo_mixed_free(self._handle)
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.nzo_mixed_free(self._handle)
 
     def codes(self):
         n = lib().nzo_mixed_symbols(self._handle)
@@ -212,8 +212,8 @@ class Huff0Table:
         return cls(lib().nzo_huf_from_lengths(bytes(lengths)))
 
     def __del__(self):
-        if getattr(self, "_handle", None):
-            lib().nzo_huf_free(self._handle)
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.nzo_huf_free(self._handle)
 
     def codes(self):
         lengths = np.zeros(256, dtype=np.uint8)
@@ -282,12 +282,14 @@ def decompress_many(specs, threads=0):
                                      table._handle if table is not None else None))
         chunk_array = (_Chunk * max(len(chunks), 1))(*chunks)
         size_array = (ctypes.c_size_t * len(sizes))(*sizes)
-        out = np.zeros(max(numel * element_size, 1), dtype=np.uint8)
-        keep.extend([chunk_array, size_array, out])
+        out = bytearray(numel * element_size)
+        view = np.frombuffer(out, dtype=np.uint8) if len(out) else np.zeros(1, np.uint8)
+        keep.extend([chunk_array, size_array, view])
         outputs.append(out)
         tensors.append(_Tensor(element_size, int(bit_reorder), numel,
                                ctypes.cast(chunk_array, ctypes.c_void_p),
-                               ctypes.cast(size_array, ctypes.c_void_p), out.ctypes.data))
+                               ctypes.cast(size_array, ctypes.c_void_p), view.ctypes.data))
     tensor_array = (_Tensor * max(len(tensors), 1))(*tensors)
     _check(lib().nzo_decompress_many(ctypes.cast(tensor_array, ctypes.c_void_p), len(tensors), int(threads)))
-    return [bytearray(out[: spec[2] * spec[0]].tobytes()) for out, spec in zip(outputs, specs)]
+    del keep
+    return outputs

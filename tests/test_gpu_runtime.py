@@ -1,0 +1,95 @@
+"""Runtime on the GPU: hooks, workspaces, prefetch and bitwise outputs
+(_experiment_kernel_checks.py:134-198, _experiment_module_checks.py:145-160)."""
+import copy
+
+import pytest
+import torch
+from torch import nn
+
+from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+from neuralzip_amd.setup import NeuralZipSetup
+
+pytestmark = pytest.mark.gpu
+
+
+class Model(nn.Module):
+    def __init__(self, dtype):
+        super().__init__()
+        self.layers = nn.ModuleList([nn.Linear(257, 513, bias=False, dtype=dtype),
+                                     nn.Linear(513, 17, bias=False, dtype=dtype)])
+
+    def forward(self, inputs):
+        for layer in self.layers:
+            inputs = layer(inputs)
+        return inputs
+
+
+def exact(a, b):
+    return torch.equal(a.cpu().contiguous().view(torch.uint8), b.cpu().contiguous().view(torch.uint8))
+
+
+def pattern(model, dtype):
+    with torch.no_grad():
+        for p in model.parameters():
+            values = torch.tensor([0.25, 0.25, 0.25, 0.25, 0.5, 0.5, 1, 1], dtype=dtype)
+            p.copy_(values.repeat((p.numel() + 7) // 8)[:p.numel()].view_as(p))
+
+
+@pytest.mark.parametrize("prefetch", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_pattern_model_with_raw_fragment(dtype, prefetch):
+    torch.manual_seed(42)
+    model = Model(dtype).eval()
+    pattern(model, dtype)
+    named = {name: p.detach().clone() for name, p in model.named_parameters()}
+    setup = NeuralZipSetup(chunk_size=8192).build(named)
+    baseline = copy.deepcopy(model).cuda()
+    inputs = torch.ones(1, 257, dtype=dtype, device="cuda")
+    expected = baseline(inputs).cpu()
+    key = next(iter(setup.chunk_codebooks))
+    ids = list(setup.chunk_codebooks[key])
+    ids[len(ids) // 2] = None                         # a raw fragment between compressed ones
+    setup.chunk_codebooks[key] = tuple(ids)
+    exported = export_model_for_gpu(model, setup)
+    assert {b.tensor_name for b in exported.bindings} == set(named)
+    if dtype is not torch.float16:
+        assert any(g.codebook.vocab for g in exported.groups), "pair route not exercised"
+    assert any(g.codebook_id == -1 for g in exported.groups)
+    runtime = NeuralZipRuntime.attach(model, exported, device="cuda:0", prefetch=prefetch)
+    assert all("weight" not in model.get_submodule(b.module_name)._parameters for b in exported.bindings)
+    for workspace in runtime.workspaces.values():
+        workspace.view(torch.uint8).fill_(0xA5)
+    restored = dict(runtime.materialized_weights())
+    assert all(exact(restored[name], t) for name, t in named.items())
+    for _ in range(3):
+        runtime.drain()
+        torch.cuda.synchronize()
+        for workspace in runtime.workspaces.values():
+            workspace.view(torch.uint8).fill_(0xA5)
+        assert exact(model(inputs), expected), "forward did not reconstruct exact weights"
+
+
+def test_prefetch_uses_distinct_slots_and_side_stream():
+    model = nn.Module()
+    model.blocks = nn.ModuleList([nn.Sequential(nn.Linear(256, 256, bias=False, dtype=torch.bfloat16),
+                                                nn.GELU()) for _ in range(5)])
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape) * 0.02)
+    named = {n: p.detach().clone() for n, p in model.named_parameters()}
+    reference = copy.deepcopy(model).cuda()
+    x = torch.randn(8, 256, dtype=torch.bfloat16, device="cuda")
+    expected = x
+    for block in reference.blocks:
+        expected = block(expected)
+    setup = NeuralZipSetup(chunk_size=65536).build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
+    order = runtime.export.block_order
+    assert len(order) == 5 and len({runtime.block_slot[n] for n in order}) == 3   # odd count: 3 slots
+    for a, b in zip(order, order[1:] + order[:1]):
+        assert runtime.block_slot[a] != runtime.block_slot[b]
+    for _ in range(4):
+        y = x
+        for block in model.blocks:
+            y = block(y)
+        assert exact(y, expected)

@@ -109,3 +109,26 @@ def test_codebook_errors_match_reference_messages():
         book = _native.Codebook(header)
         raw = segment_tensor(torch.bfloat16, np.array([0, 1, 2, 3], dtype=np.uint8))
         _native.Layout([(raw, book, 0, DTYPES[torch.bfloat16])])
+
+
+def test_trailing_window_without_steps():
+    # A final window whose range starts after the last code: the previous
+    # window's last multi-token step overran the stream end into the zero
+    # padding. Such windows emit nothing and are left out of the tiles.
+    spec = DTYPES[torch.bfloat16]
+    book = _native.Codebook(b"NZM1" + segment_lengths(12), bytes((127, 127, 125, 126)))
+    rng = np.random.default_rng(0)
+    found = False
+    for _ in range(400):
+        symbols = rng.choice([0, 1, 2], int(rng.integers(20, 300))).astype(np.uint8)
+        raw = segment_tensor(torch.bfloat16, symbols)
+        layout = _native.Layout([(raw, book, 0, spec)])
+        found |= sum(_tiles_windows(layout)) < layout.info(0)["n_windows"]
+        emulate_case([(raw, torch.bfloat16, 1 << 20, [0], 0)], {0: book}, torch.bfloat16)
+    assert found, "no trailing empty window was produced"
+
+
+def _tiles_windows(layout):
+    base = np.zeros(layout.packed_bytes + 64, dtype=np.uint8)
+    _, tiles = layout.pack(base, 0, np.zeros(1, np.uint64))
+    return [int(t["n_win"]) for t in tiles]
