@@ -80,6 +80,19 @@ def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
                       f"{decoded} bytes decoded each"}
 
 
+def copy_calibration(nbytes=1 << 30, repeats=5):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE per
+    dispatch scale the decode kernel's counters to bytes."""
+    device = torch.device("cuda:0")
+    src = torch.ones(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(repeats):
+        dst.copy_(src)
+    torch.cuda.synchronize(device)
+    print(json.dumps({"copy_bytes_per_dispatch": nbytes, "dispatches": repeats}), flush=True)
+    return 0
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -87,7 +100,11 @@ def main():
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--target-groups", type=int, default=None)
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run a plain 1 GiB device copy (calibrates HBM byte counters)")
     args = parser.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print("bench.py measures one GPU: decode needs no collective and this build runs on one device; "
               "run with --gpus 1.", file=sys.stderr)
