@@ -253,7 +253,7 @@ void build_lut(Codebook& book) {
     for (uint32_t y = 0; y < NZ_LUT_ENTRIES; ++y)
         if (single[y] >= 0) book.single[y] = static_cast<uint32_t>(single[y]) | (uint32_t(book.lengths[single[y]]) << 16);
     auto& lut = book.lut;
-    lut.assign(NZ_LUT_HEADER + NZ_LUT_ENTRIES + NZ_ESC_RECORD * esc_lengths.size() + esc.size(), 0);
+    lut.assign(NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES + NZ_ESC_RECORD * esc_lengths.size() + esc.size(), 0);
     lut[0] = static_cast<uint32_t>(esc_lengths.size());
     lut[1] = static_cast<uint32_t>(esc.size());
     lut[2] = static_cast<uint32_t>(lut.size());
@@ -265,15 +265,19 @@ void build_lut(Codebook& book) {
             const int t = single[(x << pos) & (NZ_LUT_ENTRIES - 1)];
             if (t < 0 || book.lengths[t] > NZ_LUT_BITS - pos) break;
             const unsigned w = Codebook::token_width(static_cast<unsigned>(t));
-            if (count + w > 3) break;
+            if (count + w > NZ_ENTRY_MAX_BYTES) break;
             bytes |= static_cast<uint32_t>(book.token_bytes[t]) << (8 * count);
             count += w;
             pos += book.lengths[t];
             if (pos == NZ_LUT_BITS) break;
         }
-        lut[NZ_LUT_HEADER + x] = count ? bytes | (pos << 24) | (count << 28) : 0u;
+        if (count) {
+            lut[NZ_LUT_HEADER + 2 * x] = (bytes & 0xFFu) | ((bytes & 0xFF00u) << 8) |
+                                         ((32u - pos) << NZ_ENTRY_SHIFT) | (count << NZ_ENTRY_COUNT);
+            lut[NZ_LUT_HEADER + 2 * x + 1] = ((bytes >> 16) & 0xFFu) | ((bytes >> 24) << 16);
+        }
     }
-    uint32_t* record = lut.data() + NZ_LUT_HEADER + NZ_LUT_ENTRIES;
+    uint32_t* record = lut.data() + NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
     uint32_t* tokens = record + NZ_ESC_RECORD * esc_lengths.size();
     unsigned base = 0;
     for (unsigned L : esc_lengths) {
@@ -297,21 +301,22 @@ void build_lut(Codebook& book) {
         base += static_cast<unsigned>(count);
     }
     for (size_t i = 0; i < esc.size(); ++i)
-        tokens[i] = book.token_bytes[esc[i]] | (Codebook::token_width(esc[i]) << 28);
+        tokens[i] = (book.token_bytes[esc[i]] & 0xFFu) | ((book.token_bytes[esc[i]] & 0xFF00u) << 8) |
+                    (Codebook::token_width(esc[i]) << NZ_ENTRY_COUNT);
 }
 
 }  // namespace
 
 unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* bytes, unsigned* count) {
-    const uint32_t e = lut[NZ_LUT_HEADER + static_cast<uint32_t>(window >> (64 - NZ_LUT_BITS))];
-    const unsigned len = (e >> 24) & 15u;
-    if (len) {
-        *bytes = e & 0xFFFFFFu;
-        *count = e >> 28;
-        return len;
+    const uint32_t x = static_cast<uint32_t>(window >> (64 - NZ_LUT_BITS));
+    const uint32_t e = lut[NZ_LUT_HEADER + 2 * x], e1 = lut[NZ_LUT_HEADER + 2 * x + 1];
+    if (e >> NZ_ENTRY_COUNT) {
+        *bytes = (e & 0xFFu) | ((e >> 8) & 0xFF00u) | ((e1 & 0xFFu) << 16) | (((e1 >> 16) & 0xFFu) << 24);
+        *count = e >> NZ_ENTRY_COUNT;
+        return 32u - ((e >> NZ_ENTRY_SHIFT) & 31u);
     }
     const unsigned n_len = lut[0];
-    const uint32_t* record = lut.data() + NZ_LUT_HEADER + NZ_LUT_ENTRIES;
+    const uint32_t* record = lut.data() + NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
     unsigned k = 0;
     while (k + 1 < n_len) {
         const uint64_t limit = record[NZ_ESC_RECORD * k] | static_cast<uint64_t>(record[NZ_ESC_RECORD * k + 1]) << 32;
@@ -323,8 +328,8 @@ unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* b
     const unsigned L = r[5];
     const uint32_t index = r[4] + static_cast<uint32_t>((window - first) >> (64 - L));
     const uint32_t te = record[NZ_ESC_RECORD * n_len + index];
-    *bytes = te & 0xFFFFu;
-    *count = te >> 28;
+    *bytes = (te & 0xFFu) | ((te >> 8) & 0xFF00u);
+    *count = te >> NZ_ENTRY_COUNT;
     return L;
 }
 

@@ -56,8 +56,8 @@ Codebook build_codebook(const uint8_t* header, size_t header_size,
 std::array<uint8_t, 256> huff0_lengths(const uint8_t* header, size_t size, size_t* used);
 
 // Decoder step at the head of a 64-bit window (MSB first): returns consumed
-// bits and writes the emitted bytes (1..3) into *bytes / *count. Uses the
-// LUT image exactly as the kernel does.
+// bits and writes the emitted bytes (1..4, first byte lowest) into *bytes /
+// *count. Uses the LUT image exactly as the kernel does.
 unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* bytes,
                   unsigned* count);
 

@@ -6,13 +6,16 @@
 //     codebook; the codebook's 12-bit multi-token LUT and its escape tables
 //     are staged once in LDS;
 //   * one wavefront per tile, one lane per 64-bit window: the lane restarts
-//     at its stored gap, decodes one to three exponent bytes per LUT step
-//     (a single long code through the canonical escape search), and writes
-//     them into the wavefront's LDS staging area at the position given by a
-//     ballot/mbcnt prefix scan of the stored per-window counts;
+//     at its stored gap and runs LUT steps until it has emitted its stored
+//     count of exponent bytes (one to three per step; a long code goes
+//     through the canonical escape search), writing them into the
+//     wavefront's LDS staging area at the offset given by a DPP prefix scan
+//     of the counts;
 //   * the wavefront then merges staged exponents with the raw byte lanes,
-//     undoes the sign/exponent reorder (decode.cu:83-100), and stores whole
-//     16-byte vectors; partial vectors at tile edges use element stores.
+//     undoes the sign/exponent reorder (decode.cu:83-100) with bit-field
+//     inserts, and stores whole 16-byte vectors; the elements of the (at
+//     most two) partial vectors at the tile's edges are stored by one extra
+//     lane-parallel round.
 // Every wavefront runs its tile loop independently and software-pipelines
 // it: the next tile's metadata, window bits and raw lanes are requested
 // before the current tile is decoded. The only workgroup barrier follows the
@@ -26,13 +29,18 @@
 
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / NZ_WAVE;
-
+// Wavefronts per workgroup: 16 with the 36 KB LUT image and 2 KB of staging
+// per wavefront lets two workgroups (8 wavefronts per SIMD) share a CU's LDS.
+#ifndef NZ_GROUP_WAVES
+#define NZ_GROUP_WAVES 16
+#endif
 // Minimum wavefronts per SIMD the register allocator must allow.
 #ifndef NZ_WAVES_PER_EU
-#define NZ_WAVES_PER_EU 6
+#define NZ_WAVES_PER_EU 8
 #endif
+constexpr int kWaves = NZ_GROUP_WAVES;
+constexpr int kThreads = kWaves * NZ_WAVE;
+constexpr int kIcmpUlt = 36;   // unsigned-less-than predicate of the lane-mask compare builtin
 
 __device__ __forceinline__ uint32_t bswap32(uint32_t x) { return __builtin_amdgcn_perm(0u, x, 0x00010203u); }
 
@@ -40,18 +48,34 @@ __device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t s)
     return __builtin_amdgcn_alignbit(hi, lo, s);
 }
 
-// Exclusive prefix sum over the wavefront of an 8-bit value: one ballot per
-// bit plane, mbcnt counts the set lanes below this one.
-__device__ __forceinline__ uint32_t wave_exclusive_scan8(uint32_t v) {
-    uint32_t sum = 0;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const uint64_t plane = __ballot((v >> b) & 1u);
-        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(plane >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(plane), 0u));
-        sum += below << b;
-    }
-    return sum;
+// Bit-field insert: bits of `a` where `mask` is set, bits of `b` elsewhere.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (a & mask) | (b & ~mask); }
+
+// Buffer resources: a wave-uniform base and byte range; loads outside the
+// range return zero and stores outside it are dropped, so every lane issues
+// the same memory instructions whether or not its element exists. Word 3
+// selects 32-bit raw data, the untyped layout of the gfx9 family.
+constexpr uint32_t kRawBufferFlags = 0x00020000u;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRawBufferFlags);
+}
+
+// Inclusive prefix sum over the wavefront: shifts of 1, 2, 4, 8 lanes inside
+// each row of 16, then the row carries (row_bcast:15 into rows 1 and 3,
+// row_bcast:31 into rows 2 and 3).
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xA, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xC, 0xF, false));
+    return v;
 }
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -61,10 +85,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Canonical decode of one code longer than 12 bits: find the first escape
-// length whose left-justified limit exceeds the window.
+// length whose left-justified limit exceeds the window. Returns the escape
+// token entry; *len receives the code length.
 __device__ __forceinline__ uint32_t escape_entry(const uint32_t* lut, uint64_t window, uint32_t* len) {
     const uint32_t n_len = lut[0];
-    const uint32_t* rec = lut + NZ_LUT_HEADER + NZ_LUT_ENTRIES;
+    const uint32_t* rec = lut + NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
     uint32_t k = 0;
     while (k + 1 < n_len) {
         const uint64_t limit = rec[NZ_ESC_RECORD * k] | (static_cast<uint64_t>(rec[NZ_ESC_RECORD * k + 1]) << 32);
@@ -86,50 +111,70 @@ __device__ __forceinline__ uint32_t restore_word(uint32_t v) {
     return (v & 0x007FFFFFu) | ((v << 8) & 0x80000000u) | ((v >> 1) & 0x7F800000u);
 }
 
-// One element from its exponent byte and raw lanes (partial vectors).
-template <int ES, bool REORDER>
-__device__ __forceinline__ void store_element(uint8_t* out, uint64_t g, uint8_t expo, const uint8_t* lanes,
-                                              uint32_t stride) {
-    uint32_t v = static_cast<uint32_t>(expo) << (8 * (ES - 1));
-#pragma unroll
-    for (int k = 0; k + 1 < ES; ++k) v |= static_cast<uint32_t>(lanes[k * stride]) << (8 * k);
-    if (ES == 2) {
-        *reinterpret_cast<uint16_t*>(out + g * 2) = static_cast<uint16_t>(restore_word<2, REORDER>(v));
+// Four elements' top two bytes from four exponent bytes `e` and the four
+// stored bytes below them `r` (bit 7 = sign when reordered): returns the
+// restored high bytes in *hi and the bytes below them in *lo.
+template <bool REORDER>
+__device__ __forceinline__ void restore_pairs(uint32_t e, uint32_t r, uint32_t* hi, uint32_t* lo) {
+    if (REORDER) {
+        *hi = bfi(0x7F7F7F7Fu, e >> 1, r);    // sign | exponent >> 1
+        *lo = bfi(0x7F7F7F7Fu, r, e << 7);    // exponent bit 0 | low mantissa bits
     } else {
-        *reinterpret_cast<uint32_t*>(out + g * 4) = restore_word<4, REORDER>(v);
+        *hi = e;
+        *lo = r;
     }
 }
 
-// A whole 16-byte vector: V exponent bytes (`e0`, `e1` hold 8 or 4 bytes)
-// merged with the raw lanes at `lanes` (vector aligned).
+// A whole 16-byte vector of V elements. `e` holds V exponent bytes (two
+// dwords for 2-byte words, one for 4-byte words); `r` the raw lane dwords
+// (lane 0 for 2-byte words; lanes 0, 1, 2 for 4-byte words).
 template <int ES, bool REORDER>
-__device__ __forceinline__ void store_vector(uint8_t* out, uint64_t g, uint32_t e0, uint32_t e1,
-                                             const uint8_t* lanes, uint32_t stride) {
+__device__ __forceinline__ uint4 merge_vector(uint32_t e0, uint32_t e1, const uint32_t* r) {
     uint4 v;
     if (ES == 2) {
-        const uint2 r = *reinterpret_cast<const uint2*>(lanes);
-        v.x = __builtin_amdgcn_perm(e0, r.x, 0x05010400u);
-        v.y = __builtin_amdgcn_perm(e0, r.x, 0x07030602u);
-        v.z = __builtin_amdgcn_perm(e1, r.y, 0x05010400u);
-        v.w = __builtin_amdgcn_perm(e1, r.y, 0x07030602u);
+        uint32_t hi, lo;
+        restore_pairs<REORDER>(e0, r[0], &hi, &lo);
+        v.x = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        v.y = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+        restore_pairs<REORDER>(e1, r[1], &hi, &lo);
+        v.z = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        v.w = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
     } else {
-        const uint32_t l0 = *reinterpret_cast<const uint32_t*>(lanes);
-        const uint32_t l1 = *reinterpret_cast<const uint32_t*>(lanes + stride);
-        const uint32_t l2 = *reinterpret_cast<const uint32_t*>(lanes + 2 * stride);
-        const uint32_t a = __builtin_amdgcn_perm(l1, l0, 0x05010400u);
-        const uint32_t b = __builtin_amdgcn_perm(l1, l0, 0x07030602u);
-        const uint32_t c = __builtin_amdgcn_perm(e0, l2, 0x05010400u);
-        const uint32_t d = __builtin_amdgcn_perm(e0, l2, 0x07030602u);
+        uint32_t hi, lo;
+        restore_pairs<REORDER>(e0, r[2], &hi, &lo);
+        const uint32_t a = __builtin_amdgcn_perm(r[1], r[0], 0x05010400u);
+        const uint32_t b = __builtin_amdgcn_perm(r[1], r[0], 0x07030602u);
+        const uint32_t c = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        const uint32_t d = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
         v.x = __builtin_amdgcn_perm(c, a, 0x05040100u);
         v.y = __builtin_amdgcn_perm(c, a, 0x07060302u);
         v.z = __builtin_amdgcn_perm(d, b, 0x05040100u);
         v.w = __builtin_amdgcn_perm(d, b, 0x07060302u);
     }
-    v.x = restore_word<ES, REORDER>(v.x);
-    v.y = restore_word<ES, REORDER>(v.y);
-    v.z = restore_word<ES, REORDER>(v.z);
-    v.w = restore_word<ES, REORDER>(v.w);
-    *reinterpret_cast<uint4*>(out + g * ES) = v;
+    return v;
+}
+
+// One element from its exponent byte and its raw lane bytes `raw`
+// (lane k in byte k).
+template <int ES, bool REORDER>
+__device__ __forceinline__ void store_element(uint8_t* out, uint32_t expo, uint32_t raw) {
+    const uint32_t v = restore_word<ES, REORDER>((expo << (8 * (ES - 1))) | raw);
+    if (ES == 2) {
+        *reinterpret_cast<uint16_t*>(out) = static_cast<uint16_t>(v);
+    } else {
+        *reinterpret_cast<uint32_t*>(out) = v;
+    }
+}
+
+// The same through a buffer resource (offset kOutOfRange stores nothing).
+template <int ES, bool REORDER>
+__device__ __forceinline__ void store_element(rsrc_t out, uint32_t offset, uint32_t expo, uint32_t raw) {
+    const uint32_t v = restore_word<ES, REORDER>((expo << (8 * (ES - 1))) | raw);
+    if (ES == 2) {
+        __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v), out, offset, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32(v, out, offset, 0, 0);
+    }
 }
 
 template <int ES>
@@ -147,7 +192,6 @@ struct TileInfo {
     const uint16_t* meta;      // its metadata
     const uint8_t* lanes;      // raw lane 0 at the tile's first vector
     uint8_t* out;              // output at the tile's first vector
-    uint64_t bits_left;        // fragment bits from the first window on
     uint32_t stride;           // raw lane stride
     uint32_t n_win;
     uint32_t s0, s1;           // staging indices of the first and one-past-last element
@@ -168,13 +212,20 @@ __device__ __forceinline__ TileInfo tile_info(const uint8_t* base, const nz_frag
     ti.meta = reinterpret_cast<const uint16_t*>(base + f.meta) + tile.win0;
     ti.lanes = base + f.lanes + (vbase * V - origin);
     ti.out = out + vbase * V * ES;
-    ti.bits_left = f.bit_length - 64ull * tile.win0;
     ti.stride = f.lane_stride;
     ti.n_win = nz_tile_windows(tile.counts);
     ti.s0 = static_cast<uint32_t>(a0 - vbase * V);
     ti.s1 = ti.s0 + nz_tile_elements(tile.counts);
     ti.nv = (ti.s1 + V - 1) / V;
     return ti;
+}
+
+// Staging index of the edge element lane `lane` owns in the edge round:
+// lanes [0, V) the first vector, lanes [V, 2V) the last one.
+template <int ES>
+__device__ __forceinline__ uint32_t edge_index(const TileInfo& ti, uint32_t lane) {
+    constexpr uint32_t V = Geometry<ES>::V;
+    return lane < V ? lane : (ti.nv - 1) * V + (lane & (V - 1));
 }
 
 // Everything a lane reads from global memory for one tile. All loads are
@@ -185,93 +236,105 @@ struct Fetch {
     uint32_t meta;
     uint32_t w[LONG ? 4 : 3];
     uint32_t raw[Geometry<ES>::kRounds][Geometry<ES>::kLaneWords];
+    uint32_t edge;             // raw lane bytes of this lane's edge element
 };
 
 template <int ES, bool LONG>
 __device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<ES, LONG>& d) {
     using G = Geometry<ES>;
-    const uint32_t l = lane < ti.n_win ? lane : ti.n_win - 1;
-    d.meta = ti.meta[l];
-    const uint8_t* src = ti.bits + 8u * l;
-    const uint2 p = *reinterpret_cast<const uint2*>(src);
-    d.w[0] = p.x;
-    d.w[1] = p.y;
+    const rsrc_t meta = make_rsrc(ti.meta, 2 * ti.n_win);
+    const rsrc_t bits = make_rsrc(ti.bits, 8 * ti.n_win + NZ_BITS_PAD);
+    const uint32_t span = ti.nv * G::V;   // lane bytes covering the tile's vectors
+    const rsrc_t lanes = make_rsrc(ti.lanes, ES == 2 ? span : 2 * ti.stride + span);
+    d.meta = __builtin_amdgcn_raw_buffer_load_b16(meta, 2 * lane, 0, 0);
     if (LONG) {
-        const uint2 q = *reinterpret_cast<const uint2*>(src + 8);
-        d.w[2] = q.x;
-        d.w[3] = q.y;
+        const v4u w = __builtin_amdgcn_raw_buffer_load_b128(bits, 8 * lane, 0, 0);
+        d.w[0] = w.x;
+        d.w[1] = w.y;
+        d.w[2] = w.z;
+        d.w[3] = w.w;
     } else {
-        d.w[2] = *reinterpret_cast<const uint32_t*>(src + 8);
+        const v2u w = __builtin_amdgcn_raw_buffer_load_b64(bits, 8 * lane, 0, 0);
+        d.w[0] = w.x;
+        d.w[1] = w.y;
+        d.w[2] = __builtin_amdgcn_raw_buffer_load_b32(bits, 8 * lane + 8, 0, 0);
     }
 #pragma unroll
     for (uint32_t r = 0; r < G::kRounds; ++r) {
-        uint32_t i = lane + NZ_WAVE * r;
-        i = i < ti.nv ? i : ti.nv - 1;
-        const uint8_t* lanes = ti.lanes + i * G::V;
+        const uint32_t at = (lane + NZ_WAVE * r) * G::V;
         if (ES == 2) {
-            const uint2 v = *reinterpret_cast<const uint2*>(lanes);
+            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(lanes, at, 0, 0);
             d.raw[r][0] = v.x;
             d.raw[r][1] = v.y;
         } else {
-            d.raw[r][0] = *reinterpret_cast<const uint32_t*>(lanes);
-            d.raw[r][1] = *reinterpret_cast<const uint32_t*>(lanes + ti.stride);
-            d.raw[r][2] = *reinterpret_cast<const uint32_t*>(lanes + 2 * ti.stride);
+            d.raw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(lanes, at, 0, 0);
+            d.raw[r][1] = __builtin_amdgcn_raw_buffer_load_b32(lanes, at + ti.stride, 0, 0);
+            d.raw[r][2] = __builtin_amdgcn_raw_buffer_load_b32(lanes, at + 2 * ti.stride, 0, 0);
         }
     }
-}
-
-template <int ES, bool REORDER>
-__device__ __forceinline__ void store_vector_regs(uint8_t* out, uint32_t e0, uint32_t e1, const uint32_t* r) {
-    uint4 v;
+    const uint32_t g = lane < 2 * G::V ? edge_index<ES>(ti, lane) : kOutOfRange;
     if (ES == 2) {
-        v.x = __builtin_amdgcn_perm(e0, r[0], 0x05010400u);
-        v.y = __builtin_amdgcn_perm(e0, r[0], 0x07030602u);
-        v.z = __builtin_amdgcn_perm(e1, r[1], 0x05010400u);
-        v.w = __builtin_amdgcn_perm(e1, r[1], 0x07030602u);
+        d.edge = __builtin_amdgcn_raw_buffer_load_b8(lanes, g, 0, 0);
     } else {
-        const uint32_t a = __builtin_amdgcn_perm(r[1], r[0], 0x05010400u);
-        const uint32_t b = __builtin_amdgcn_perm(r[1], r[0], 0x07030602u);
-        const uint32_t c = __builtin_amdgcn_perm(e0, r[2], 0x05010400u);
-        const uint32_t d = __builtin_amdgcn_perm(e0, r[2], 0x07030602u);
-        v.x = __builtin_amdgcn_perm(c, a, 0x05040100u);
-        v.y = __builtin_amdgcn_perm(c, a, 0x07060302u);
-        v.z = __builtin_amdgcn_perm(d, b, 0x05040100u);
-        v.w = __builtin_amdgcn_perm(d, b, 0x07060302u);
-    }
-    v.x = restore_word<ES, REORDER>(v.x);
-    v.y = restore_word<ES, REORDER>(v.y);
-    v.z = restore_word<ES, REORDER>(v.z);
-    v.w = restore_word<ES, REORDER>(v.w);
-    *reinterpret_cast<uint4*>(out) = v;
-}
-
-// Element j of a vector from registers (tile edges).
-template <int ES, bool REORDER>
-__device__ __forceinline__ void store_element_regs(uint8_t* out, uint32_t j, uint8_t expo, const uint32_t* r) {
-    uint32_t v = static_cast<uint32_t>(expo) << (8 * (ES - 1));
-    if (ES == 2) {
-        v |= (r[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        *reinterpret_cast<uint16_t*>(out + 2 * j) = static_cast<uint16_t>(restore_word<2, REORDER>(v));
-    } else {
-        v |= ((r[0] >> (8 * j)) & 0xFFu) | (((r[1] >> (8 * j)) & 0xFFu) << 8) | (((r[2] >> (8 * j)) & 0xFFu) << 16);
-        *reinterpret_cast<uint32_t*>(out + 4 * j) = restore_word<4, REORDER>(v);
+        d.edge = __builtin_amdgcn_raw_buffer_load_b8(lanes, g, 0, 0) |
+                 (static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(lanes, g + ti.stride, 0, 0)) << 8) |
+                 (static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(lanes, g + 2 * ti.stride, 0, 0)) << 16);
     }
 }
 
-template <int ES, bool REORDER, bool LONG>
+// One LUT step at the head of the window w0..w3: writes four bytes at *p
+// (only the entry's count of them is meaningful; the rest are overwritten
+// by the lane's next step or repaired after the loop), advances *p by the
+// count and shifts the window by the consumed bits. Returns the entry.
+template <bool LONG, bool ESC>
+__device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint32_t& w0, uint32_t& w1,
+                                          uint32_t& w2, uint32_t& w3) {
+    uint2 e = reinterpret_cast<const uint2*>(lut + NZ_LUT_HEADER)[w0 >> (32 - NZ_LUT_BITS)];
+    uint32_t s = e.x >> NZ_ENTRY_SHIFT;   // the funnel shift reads its low five bits
+    if (ESC) {
+        // wave-uniform test first (one compare into a lane mask): escapes are rare
+        if (__builtin_amdgcn_uicmp(e.x, 1u << NZ_ENTRY_COUNT, kIcmpUlt)) {
+            if (e.x < (1u << NZ_ENTRY_COUNT)) {
+                uint32_t len;
+                e.x = escape_entry(lut, (static_cast<uint64_t>(w0) << 32) | w1, &len);
+                if (LONG && len > 32) {
+                    w0 = w1;
+                    w1 = w2;
+                    w2 = w3;
+                    w3 = 0;
+                    len -= 32;
+                }
+                s = 32 - len;   // len in [1, 32]; s == 0 shifts a whole word
+            }
+        }
+    }
+    p[0] = static_cast<uint8_t>(e.x);
+    p[1] = static_cast<uint8_t>(e.x >> 16);
+    p[2] = static_cast<uint8_t>(e.y);
+    p[3] = static_cast<uint8_t>(e.y >> 16);
+    p += e.x >> NZ_ENTRY_COUNT;
+    w0 = funnel(w0, w1, s);
+    w1 = funnel(w1, w2, s);
+    w2 = funnel(w2, LONG ? w3 : 0u, s);
+    if (LONG) w3 = funnel(w3, 0u, s);
+    return e;
+}
+
+// The entry's bytes b0..b3 packed into one dword, first byte lowest.
+__device__ __forceinline__ uint32_t entry_bytes(uint2 e) { return __builtin_amdgcn_perm(e.y, e.x, 0x06040200u); }
+
+template <int ES, bool REORDER, bool LONG, bool ESC>
 __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES, LONG>& d, const uint32_t* lut,
                                              uint8_t* stage, uint32_t lane) {
     using G = Geometry<ES>;
-    const bool active = lane < ti.n_win;
-    const uint32_t gap = d.meta & 0xFFu;
-    const uint32_t offset = wave_exclusive_scan8(active ? d.meta >> 8 : 0u);
-    if (active) {
+    constexpr uint32_t V = G::V;
+    const uint32_t count = lane < ti.n_win ? d.meta >> 8 : 0u;
+    const uint32_t offset = wave_inclusive_scan(count) - count;
+    uint8_t* const first = stage + ti.s0 + offset;
+    if (count) {
         uint32_t w0 = bswap32(d.w[0]), w1 = bswap32(d.w[1]), w2 = bswap32(d.w[2]), w3 = LONG ? bswap32(d.w[3]) : 0u;
-        const uint64_t remaining = ti.bits_left - 64ull * lane;
-        const uint32_t end = remaining < 64 ? static_cast<uint32_t>(remaining) : 64u;
-        uint32_t pos = gap;
         {   // restart at the gap
-            uint32_t g = gap;
+            uint32_t g = d.meta & 0xFFu;
             if (LONG && g >= 32) { w0 = w1; w1 = w2; w2 = w3; w3 = 0; g -= 32; }
             if (g) {
                 const uint32_t s = 32 - g;
@@ -281,48 +344,55 @@ __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES,
                 if (LONG) w3 = funnel(w3, 0u, s);
             }
         }
-        uint32_t o = ti.s0 + offset;
-        while (pos < end) {
-            uint32_t e = lut[NZ_LUT_HEADER + (w0 >> (32 - NZ_LUT_BITS))];
-            uint32_t len = (e >> 24) & 15u;
-            if (len == 0) e = escape_entry(lut, (static_cast<uint64_t>(w0) << 32) | w1, &len);
-            const uint32_t n = e >> 28;
-            stage[o] = static_cast<uint8_t>(e);
-            if (n > 1) stage[o + 1] = static_cast<uint8_t>(e >> 8);
-            if (n > 2) stage[o + 2] = static_cast<uint8_t>(e >> 16);
-            o += n;
-            pos += len;
-            if (LONG && len >= 32) { w0 = w1; w1 = w2; w2 = w3; w3 = 0; len -= 32; }
-            if (!LONG || len) {
-                const uint32_t s = 32 - len;   // len in [1, 32]; s == 0 shifts a whole word
-                w0 = funnel(w0, w1, s);
-                w1 = funnel(w1, w2, s);
-                w2 = funnel(w2, LONG ? w3 : 0u, s);
-                if (LONG) w3 = funnel(w3, 0u, s);
+        uint8_t* p = first;
+        uint8_t* const end = first + count;
+        // The previous lane's last step may spill three bytes over this
+        // lane's first three; keep them and write them again after the loop.
+        // Every step emits at least one byte, so three steps cover them.
+        uint32_t head = entry_bytes(lut_step<LONG, ESC>(lut, p, w0, w1, w2, w3));
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t have = static_cast<uint32_t>(p - first);
+            if (have < 3 && p < end) {
+                const uint32_t bits = 8 * have;
+                const uint32_t more = entry_bytes(lut_step<LONG, ESC>(lut, p, w0, w1, w2, w3));
+                head = (head & ((1u << bits) - 1u)) | (more << bits);
             }
         }
+        while (p < end) lut_step<LONG, ESC>(lut, p, w0, w1, w2, w3);
+        first[0] = static_cast<uint8_t>(head);
+        if (count > 1) first[1] = static_cast<uint8_t>(head >> 8);
+        if (count > 2) first[2] = static_cast<uint8_t>(head >> 16);
     }
     wave_lds_sync();
+    // Every lane issues every store; lanes without a whole vector (or edge
+    // element) aim outside the buffer range and store nothing, so the
+    // number of memory instructions per tile is fixed and waiting for the
+    // next tile's loads never waits for these stores.
+    const rsrc_t out = make_rsrc(ti.out, ti.nv * 16u);
 #pragma unroll
     for (uint32_t r = 0; r < G::kRounds; ++r) {
-        const uint32_t i = lane + NZ_WAVE * r;
-        if (i >= ti.nv) break;
-        const uint32_t g = i * G::V;
-        uint8_t* out = ti.out + g * ES;
-        if (g >= ti.s0 && g + G::V <= ti.s1) {
-            uint32_t e0, e1 = 0;
-            if (ES == 2) {
-                const uint2 e = *reinterpret_cast<const uint2*>(stage + g);
-                e0 = e.x;
-                e1 = e.y;
-            } else {
-                e0 = *reinterpret_cast<const uint32_t*>(stage + g);
-            }
-            store_vector_regs<ES, REORDER>(out, e0, e1, d.raw[r]);
+        const uint32_t g = (lane + NZ_WAVE * r) * V;
+        const bool whole = g >= ti.s0 && g + V <= ti.s1;
+        const uint32_t at = whole ? g : 0u;
+        uint32_t e0, e1 = 0;
+        if (ES == 2) {
+            const uint2 e = *reinterpret_cast<const uint2*>(stage + at);
+            e0 = e.x;
+            e1 = e.y;
         } else {
-            for (uint32_t j = 0; j < G::V; ++j)
-                if (g + j >= ti.s0 && g + j < ti.s1) store_element_regs<ES, REORDER>(out, j, stage[g + j], d.raw[r]);
+            e0 = *reinterpret_cast<const uint32_t*>(stage + at);
         }
+        const uint4 v = merge_vector<ES, REORDER>(e0, e1, d.raw[r]);
+        const v4u vv = {v.x, v.y, v.z, v.w};
+        __builtin_amdgcn_raw_buffer_store_b128(vv, out, whole ? g * ES : kOutOfRange, 0, 0);
+    }
+    {   // elements of the partial first and last vectors
+        const uint32_t g = edge_index<ES>(ti, lane);
+        const uint32_t vec0 = g & ~(V - 1);
+        const bool partial = !(vec0 >= ti.s0 && vec0 + V <= ti.s1);
+        const bool mine = lane < 2 * V && (lane < V || ti.nv > 1) && partial && g >= ti.s0 && g < ti.s1;
+        store_element<ES, REORDER>(out, mine ? g * ES : kOutOfRange, stage[mine ? g : 0u], d.edge);
     }
     wave_lds_sync();
 }
@@ -340,20 +410,53 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
         const uint8_t* expo = base + f.bits + (g - origin);
         const uint8_t* lanes = base + f.lanes + (g - origin);
         if (g >= A0 && g + V <= A1) {
-            uint32_t e0, e1 = 0;
+            uint32_t e0, e1 = 0, r[3];
             if (ES == 2) {
                 const uint2 e = *reinterpret_cast<const uint2*>(expo);
                 e0 = e.x;
                 e1 = e.y;
+                const uint2 l = *reinterpret_cast<const uint2*>(lanes);
+                r[0] = l.x;
+                r[1] = l.y;
             } else {
                 e0 = *reinterpret_cast<const uint32_t*>(expo);
+                r[0] = *reinterpret_cast<const uint32_t*>(lanes);
+                r[1] = *reinterpret_cast<const uint32_t*>(lanes + f.lane_stride);
+                r[2] = *reinterpret_cast<const uint32_t*>(lanes + 2 * f.lane_stride);
             }
-            store_vector<ES, REORDER>(out, g, e0, e1, lanes, f.lane_stride);
+            *reinterpret_cast<uint4*>(out + g * ES) = merge_vector<ES, REORDER>(e0, e1, r);
         } else {
-            for (uint32_t j = 0; j < V; ++j)
-                if (g + j >= A0 && g + j < A1)
-                    store_element<ES, REORDER>(out, g + j, expo[j], lanes + j, f.lane_stride);
+            for (uint32_t j = 0; j < V; ++j) {
+                if (g + j >= A0 && g + j < A1) {
+                    uint32_t raw = 0;
+                    for (int k = 0; k + 1 < ES; ++k) raw |= static_cast<uint32_t>(lanes[j + k * f.lane_stride]) << (8 * k);
+                    store_element<ES, REORDER>(out + (g + j) * ES, expo[j], raw);
+                }
+            }
         }
+    }
+}
+
+template <int ES, bool REORDER, bool LONG, bool ESC>
+__device__ __forceinline__ void huffman_tiles(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                                              const nz_work& wk, uint32_t wave, uint32_t lane, const uint32_t* lut,
+                                              uint8_t* stage, uint8_t* out) {
+    uint32_t t = wk.tile0 + wave;
+    if (t >= wk.tile1) return;
+    TileInfo cur = tile_info<ES>(base, frags, tiles, t, out);
+    Fetch<ES, LONG> fc;
+    fetch<ES, LONG>(cur, lane, fc);
+    for (;;) {
+        const uint32_t tn = t + kWaves;
+        const bool more = tn < wk.tile1;
+        const TileInfo nxt = tile_info<ES>(base, frags, tiles, more ? tn : t, out);
+        Fetch<ES, LONG> fn;
+        fetch<ES, LONG>(nxt, lane, fn);
+        huffman_tile<ES, REORDER, LONG, ESC>(cur, fc, lut, stage, lane);
+        if (!more) break;
+        t = tn;
+        cur = nxt;
+        fc = fn;
     }
 }
 
@@ -376,32 +479,26 @@ void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
         }
         return;
     }
+    const uint4* img = reinterpret_cast<const uint4*>(base + frags[wk.lut_frag].lut);
+    const uint32_t escapes = reinterpret_cast<const uint32_t*>(img)[0];
     {
-        const uint4* img = reinterpret_cast<const uint4*>(base + frags[wk.lut_frag].lut);
         const uint32_t words = reinterpret_cast<const uint32_t*>(img)[2];
         uint4* dst = reinterpret_cast<uint4*>(s_lut);
         for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kThreads) dst[i] = img[i];
         __syncthreads();
     }
-    uint8_t* stage = s_stage[wave];
-    uint32_t t = wk.tile0 + wave;
-    if (t >= wk.tile1) return;
-    TileInfo cur = tile_info<ES>(base, frags, tiles, t, out);
-    Fetch<ES, LONG> fc;
-    fetch<ES, LONG>(cur, lane, fc);
-    for (;;) {
-        const uint32_t tn = t + kWaves;
-        const bool more = tn < wk.tile1;
-        const TileInfo nxt = tile_info<ES>(base, frags, tiles, more ? tn : t, out);
-        Fetch<ES, LONG> fn;
-        fetch<ES, LONG>(nxt, lane, fn);
-        huffman_tile<ES, REORDER, LONG>(cur, fc, s_lut, stage, lane);
-        if (!more) break;
-        t = tn;
-        cur = nxt;
-        fc = fn;
+    // Codebooks whose codes all fit the primary table run the loop without
+    // the escape check (long-code codebooks always have escapes).
+    if constexpr (LONG) {
+        huffman_tiles<ES, REORDER, true, true>(base, frags, tiles, wk, wave, lane, s_lut, s_stage[wave], out);
+    } else {
+        if (escapes)
+            huffman_tiles<ES, REORDER, false, true>(base, frags, tiles, wk, wave, lane, s_lut, s_stage[wave], out);
+        else
+            huffman_tiles<ES, REORDER, false, false>(base, frags, tiles, wk, wave, lane, s_lut, s_stage[wave], out);
     }
 }
+
 template <int ES, bool REORDER, bool LONG>
 hipError_t launch(const void* base, const void* frags, const void* tiles, const void* work, uint32_t n_work,
                   void* out, hipStream_t stream) {

@@ -41,15 +41,24 @@
 // LUT image (uint32 words), uploaded once per codebook:
 //   [0] number of escape lengths E   [1] number of escape tokens T
 //   [2] image size in words           [3] longest code length
-//   [4, 4 + 4096)  primary entries
+//   [4, 4 + 2 * 4096)  primary entries, two words each
 //   then E records of 6 words: limit(lo,hi) first(lo,hi) base length
-//   then T escape token entries
-// Primary entry: bytes b0 | b1 << 8 | b2 << 16, consumed bits << 24
-// (1..12; 0 marks an escape), byte count << 28 (1..3).
-// Escape token entry: bytes | byte count << 28.
+//   then T escape token entries (one word)
+// A primary entry decodes every whole token that fits the 12-bit prefix, up
+// to four exponent bytes b0..b3:
+//   word 0: b0 | b1 << 16 | (32 - consumed bits) << 24 | byte count << 29
+//   word 1: b2 | b3 << 16
+// (consumed 1..12; byte count 1..4, 0 marks an escape). The bytes sit where
+// 8-bit stores of the low and high half-words pick them up, and the shift
+// field is what the decoder's funnel shift takes directly (it reads the low
+// five bits of its shift operand).
+// Escape token entry: b0 | b1 << 16 | byte count << 29.
 #define NZ_LUT_HEADER 4
 #define NZ_ESC_RECORD 6
-#define NZ_LUT_MAX_WORDS (NZ_LUT_HEADER + NZ_LUT_ENTRIES + NZ_ESC_RECORD * 56 + 512)
+#define NZ_ENTRY_SHIFT 24
+#define NZ_ENTRY_COUNT 29
+#define NZ_ENTRY_MAX_BYTES 4
+#define NZ_LUT_MAX_WORDS (NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES + NZ_ESC_RECORD * 56 + 512)
 
 enum nz_kind : uint32_t { NZ_KIND_RAW = 0, NZ_KIND_SHORT = 1, NZ_KIND_LONG = 2 };
 

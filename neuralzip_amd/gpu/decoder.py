@@ -16,8 +16,9 @@ from neuralzip_amd._native import FRAG_DESC, KIND_LONG, KIND_RAW, TILE
 
 THREADS_PER_BLOCK = 256
 WINDOW_BITS = 64
-# Workgroups per launch the work planner aims at: several per CU on 256 CUs.
-TARGET_GROUPS = 2048
+# Workgroups per launch the work planner aims at: four per CU on 256 CUs
+# (two 16-wavefront workgroups fit a CU at a time).
+TARGET_GROUPS = 1024
 
 
 def _align(value, alignment=256):
