@@ -99,7 +99,8 @@ def main():
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--target-groups", type=int, default=None)
+    parser.add_argument("--slots", type=int, default=None,
+                        help="decode workgroups per launch (default: what the device runs at once)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain 1 GiB device copy (calibrates HBM byte counters)")
     args = parser.parse_args()
@@ -141,8 +142,7 @@ def main():
     kinds = {}
     for f in range(len(store.descs)):
         kinds.setdefault(int(store.descs[f]["kind"]) == KIND_LONG, []).append(f)
-    target = args.target_groups or gpu_decoder.TARGET_GROUPS
-    batches = [decoder.prepare_batch(store, members, spec, workspace, target_groups=target)
+    batches = [decoder.prepare_batch(store, members, spec, workspace, slots=args.slots)
                for _, members in sorted(kinds.items())]
     decoded_bytes = sum(int(d["numel"]) for d in store.descs) * spec.element_size
     stream = torch.cuda.current_stream(device)

@@ -119,29 +119,40 @@ int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base,
                    const uint64_t* lut_offsets, uint32_t frag_base,
                    nz_frag_desc* descs, nz_tile* tiles);
 
-/* Splits tiles into workgroup ranges of one codebook and kind, aiming at
- * about `target_groups` workgroups. Writes at most `capacity` items.
- * Replaces: the block→group / block→local id tensors (decoder.py:168-179). */
-int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
-                 uint32_t target_groups, nz_work* work, uint32_t capacity, uint32_t* n_work);
+/* Launch plan over tiles whose fragments are ordered so that tiles of one
+ * LUT and kind are adjacent: one segment (nz_work record: a contiguous tile
+ * range of one LUT and kind) per workgroup. Maximal runs of one LUT and kind
+ * share out `slots` workgroups (the number the device runs at once, from
+ * nz_decode_slots; at least one per run) in proportion to their elements and
+ * are cut into that many segments of about equal elements. With
+ * segments == NULL only *n_segments is set.
+ * Replaces: the block->group / block->local id tensors (decoder.py:168-179). */
+int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
+                 nz_work* segments, uint32_t capacity, uint32_t* n_segments);
+
+/* Workgroups of the decode kernel the current HIP device runs at once
+ * (compute units x resident workgroups per unit). No reference counterpart:
+ * the reference launches one CTA per 4 KiB block (decoder.py:193-208). */
+int nz_decode_slots(int element_size, int bit_reorder, int long_codes, int* slots);
 
 /* ---- decode ----------------------------------------------------------- */
 
-/* Decodes the tiles named by `work` (device arrays) into the output
- * workspace `out` (device), on HIP stream `stream` (NULL: default stream).
- * `base` is the packed device buffer. long_codes selects the variant for
- * codes of 33..56 bits; element_size/bit_reorder select the word layout
- * (2/1 bfloat16, 2/0 float16, 4/1 float32).
+/* Decodes every tile of the plan's segments into the output workspace `out`
+ * (device), one workgroup per segment, on HIP stream `stream` (NULL: default
+ * stream). `base` is the packed device buffer; `frags`, `tiles` and
+ * `segments` are device copies of the descriptors. long_codes selects the
+ * variant for codes of 33..56 bits; element_size/bit_reorder select the word
+ * layout (2/1 bfloat16, 2/0 float16, 4/1 float32).
  * Replaces: CuPyDecoder.decode_batch (decoder.py:193-208) launching
  * decode_batched (gpu/cuda/decode.cu:323-381). */
-int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles,
-                     const nz_work* work, uint32_t n_work, int element_size, int bit_reorder,
-                     int long_codes, void* out, void* stream);
+int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
+                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
+                     void* stream);
 
 /* CPU emulation of nz_decode_launch on host copies of the same arrays; a
  * test hook for GPU-less hosts, never used by the runtime. */
 int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
-                      const nz_work* work, uint32_t n_work, int element_size, int bit_reorder,
+                      const nz_work* segments, uint32_t n_segments, int element_size, int bit_reorder,
                       uint8_t* out);
 
 /* ---- storage format (host codecs) -------------------------------------- */

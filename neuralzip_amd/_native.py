@@ -13,8 +13,19 @@ LIBRARY = Path(__file__).resolve().parent / "libneuralzip_hip.so"
 FRAG_DESC = np.dtype([("bits", "<u8"), ("meta", "<u8"), ("lanes", "<u8"), ("out", "<u8"), ("lut", "<u8"),
                       ("bit_length", "<u8"), ("numel", "<u4"), ("lane_stride", "<u4"), ("kind", "<u4"),
                       ("reserved", "<u4")])
-TILE = np.dtype([("frag", "<u4"), ("win0", "<u4"), ("out0", "<u4"), ("n_win", "<u2"), ("n_out", "<u2")])
-# (n_win, n_out) are the low and high halves of the little-endian `counts` word
+TILE = np.dtype([("frag", "<u4"), ("win0", "<u4"), ("out0", "<u4"), ("shape", "<u2"), ("n_out", "<u2")])
+# `shape` and `n_out` are the low and high halves of the little-endian `counts`
+# word: shape = windows | skipped bytes << 7.
+
+
+def tile_windows(tiles):
+    return tiles["shape"] & 0x7F
+
+
+def tile_skip(tiles):
+    return (tiles["shape"] >> 7) & 0xFF
+
+
 WORK = np.dtype([("tile0", "<u4"), ("tile1", "<u4"), ("lut_frag", "<u4"), ("kind", "<u4")])
 assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16
 
@@ -48,7 +59,8 @@ class _Totals(ctypes.Structure):
 _lib = None
 EXPORTS = ("nz_last_error", "nz_abi_version", "nz_codebook_create", "nz_codebook_destroy", "nz_codebook_export",
            "nz_codebook_lut", "nz_layout_encode", "nz_layout_destroy", "nz_layout_totals_get",
-           "nz_layout_fragment_info", "nz_layout_pack", "nz_plan_work", "nz_decode_launch", "nz_emulate_decode")
+           "nz_layout_fragment_info", "nz_layout_pack", "nz_plan_work", "nz_decode_slots", "nz_decode_launch",
+           "nz_emulate_decode")
 
 
 def lib():
@@ -71,6 +83,7 @@ def lib():
         L.nz_layout_fragment_info.argtypes = [vp, sz, ctypes.POINTER(_FragmentInfo)]
         L.nz_layout_pack.argtypes = [vp, vp, u64, vp, u32, vp, vp]
         L.nz_plan_work.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32)]
+        L.nz_decode_slots.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         _lib = L
@@ -175,22 +188,30 @@ class Layout:
         return descs, tiles
 
 
-def plan_work(descs, tiles, target_groups):
+def plan_work(descs, tiles, slots):
+    """The launch's segments (WORK records), one per workgroup."""
     n = ctypes.c_uint32()
-    check(lib().nz_plan_work(descs.ctypes.data, tiles.ctypes.data if len(tiles) else None, len(tiles),
-                             int(target_groups), None, 0, ctypes.byref(n)))
-    work = np.zeros(n.value, dtype=WORK)
-    check(lib().nz_plan_work(descs.ctypes.data, tiles.ctypes.data if len(tiles) else None, len(tiles),
-                             int(target_groups), work.ctypes.data, n.value, ctypes.byref(n)))
-    return work
+    tp = tiles.ctypes.data if len(tiles) else None
+    check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), None, 0, ctypes.byref(n)))
+    segments = np.zeros(n.value, dtype=WORK)
+    check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), segments.ctypes.data, n.value,
+                             ctypes.byref(n)))
+    return segments
 
 
-def decode_launch(base_ptr, frags_ptr, tiles_ptr, work_ptr, n_work, element_size, bit_reorder, long_codes,
+def decode_slots(element_size, bit_reorder, long_codes):
+    """Workgroups of the decode kernel the current device runs at once."""
+    n = ctypes.c_int()
+    check(lib().nz_decode_slots(int(element_size), int(bit_reorder), int(long_codes), ctypes.byref(n)))
+    return n.value
+
+
+def decode_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, element_size, bit_reorder, long_codes,
                   out_ptr, stream_ptr):
-    check(lib().nz_decode_launch(base_ptr, frags_ptr, tiles_ptr, work_ptr, int(n_work), int(element_size),
+    check(lib().nz_decode_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, int(n_segments), int(element_size),
                                  int(bit_reorder), int(long_codes), out_ptr, stream_ptr))
 
 
-def emulate_decode(base, descs, tiles, work, element_size, bit_reorder, out):
-    check(lib().nz_emulate_decode(base.ctypes.data, descs.ctypes.data, tiles.ctypes.data, work.ctypes.data,
-                                  len(work), int(element_size), int(bit_reorder), out.ctypes.data))
+def emulate_decode(base, descs, tiles, segments, element_size, bit_reorder, out):
+    check(lib().nz_emulate_decode(base.ctypes.data, descs.ctypes.data, tiles.ctypes.data, segments.ctypes.data,
+                                  len(segments), int(element_size), int(bit_reorder), out.ctypes.data))

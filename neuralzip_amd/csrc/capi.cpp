@@ -35,9 +35,11 @@ using nz_capi::guarded;
 using nz_capi::parallel_for;
 using nz_capi::set_error;
 
-extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* work,
-                                    uint32_t n_work, int element_size, int bit_reorder, int long_codes,
-                                    void* out, void* stream, char* message, size_t message_size);
+extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* segs,
+                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes, void* out,
+                                    void* stream, char* message, size_t message_size);
+extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_codes, int* out, char* message,
+                                   size_t message_size);
 
 extern "C" {
 
@@ -170,34 +172,45 @@ int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base, con
     });
 }
 
-int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t target_groups,
-                 nz_work* work, uint32_t capacity, uint32_t* n_work) {
+int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
+                 nz_work* segments, uint32_t capacity, uint32_t* n_segments) {
     return guarded([&] {
-        if (!frags || (!tiles && n_tiles) || !n_work) nz::fail(nz::kInvalidArgument, "Null plan argument.");
-        const auto plan = nz::plan_work(frags, tiles, n_tiles, target_groups);
-        *n_work = static_cast<uint32_t>(plan.size());
-        if (work) {
-            if (plan.size() > capacity) nz::fail(nz::kInvalidArgument, "Work buffer is too small.");
-            std::copy(plan.begin(), plan.end(), work);
+        if (!frags || (!tiles && n_tiles) || !n_segments) nz::fail(nz::kInvalidArgument, "Null plan argument.");
+        const auto plan = nz::plan_work(frags, tiles, n_tiles, slots);
+        *n_segments = static_cast<uint32_t>(plan.size());
+        if (segments) {
+            if (plan.size() > capacity) nz::fail(nz::kInvalidArgument, "Segment buffer is too small.");
+            std::copy(plan.begin(), plan.end(), segments);
         }
     });
 }
 
-int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* work,
-                     uint32_t n_work, int element_size, int bit_reorder, int long_codes, void* out, void* stream) {
+int nz_decode_slots(int element_size, int bit_reorder, int long_codes, int* slots) {
+    if (!slots) return set_error(nz::kInvalidArgument, "Null slots argument.");
     char message[256] = {0};
-    const int rc = nz_hip_decode_launch(base, frags, tiles, work, n_work, element_size, bit_reorder, long_codes,
-                                        out, stream, message, sizeof message);
+    const int rc = nz_hip_decode_slots(element_size, bit_reorder, long_codes, slots, message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }
 
-int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* work,
-                      uint32_t n_work, int element_size, int bit_reorder, uint8_t* out) {
+int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
+                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
+                     void* stream) {
+    if (n_segments && (!base || !frags || !tiles || !segments || !out))
+        return set_error(nz::kInvalidArgument, "Null decode argument.");
+    char message[256] = {0};
+    const int rc = nz_hip_decode_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
+                                        long_codes, out, stream, message, sizeof message);
+    if (rc) return set_error(rc, message);
+    return 0;
+}
+
+int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                      const nz_work* segments, uint32_t n_segments, int element_size, int bit_reorder, uint8_t* out) {
     return guarded([&] {
         if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
-        nz::emulate_decode(base, frags, tiles, work, n_work, static_cast<unsigned>(element_size), bit_reorder != 0,
-                           out);
+        nz::emulate_decode(base, frags, tiles, segments, n_segments, static_cast<unsigned>(element_size),
+                           bit_reorder != 0, out);
     });
 }
 

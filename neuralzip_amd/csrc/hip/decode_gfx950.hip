@@ -181,8 +181,10 @@ template <int ES>
 struct Geometry {
     static constexpr uint32_t V = 16 / ES;                        // elements per 16-byte vector
     static constexpr uint32_t kCapacity = ES == 4 ? NZ_TILE_OUT32 : NZ_TILE_OUT;
-    static constexpr uint32_t kStage = kCapacity + 32;
-    static constexpr uint32_t kRounds = (kCapacity / V + 2 + NZ_WAVE - 1) / NZ_WAVE;
+    static constexpr uint32_t kStage = NZ_STAGE_ORIGIN + kCapacity + NZ_STAGE_SLACK;
+    // a tile's vectors (its first element's offset in its vector included)
+    // never exceed the capacity
+    static constexpr uint32_t kRounds = kCapacity / V / NZ_WAVE;
     static constexpr uint32_t kLaneWords = ES == 2 ? 2 : 3;       // raw-lane dwords per vector
 };
 
@@ -194,6 +196,7 @@ struct TileInfo {
     uint8_t* out;              // output at the tile's first vector
     uint32_t stride;           // raw lane stride
     uint32_t n_win;
+    uint32_t skip;             // bytes of the first window that belong to the previous tile
     uint32_t s0, s1;           // staging indices of the first and one-past-last element
     uint32_t nv;               // vectors covering [s0, s1)
 };
@@ -214,6 +217,7 @@ __device__ __forceinline__ TileInfo tile_info(const uint8_t* base, const nz_frag
     ti.out = out + vbase * V * ES;
     ti.stride = f.lane_stride;
     ti.n_win = nz_tile_windows(tile.counts);
+    ti.skip = nz_tile_skip(tile.counts);
     ti.s0 = static_cast<uint32_t>(a0 - vbase * V);
     ti.s1 = ti.s0 + nz_tile_elements(tile.counts);
     ti.nv = (ti.s1 + V - 1) / V;
@@ -247,17 +251,12 @@ __device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<E
     const uint32_t span = ti.nv * G::V;   // lane bytes covering the tile's vectors
     const rsrc_t lanes = make_rsrc(ti.lanes, ES == 2 ? span : 2 * ti.stride + span);
     d.meta = __builtin_amdgcn_raw_buffer_load_b16(meta, 2 * lane, 0, 0);
-    if (LONG) {
+    {   // the lane's window and the 64 bits after it
         const v4u w = __builtin_amdgcn_raw_buffer_load_b128(bits, 8 * lane, 0, 0);
         d.w[0] = w.x;
         d.w[1] = w.y;
         d.w[2] = w.z;
-        d.w[3] = w.w;
-    } else {
-        const v2u w = __builtin_amdgcn_raw_buffer_load_b64(bits, 8 * lane, 0, 0);
-        d.w[0] = w.x;
-        d.w[1] = w.y;
-        d.w[2] = __builtin_amdgcn_raw_buffer_load_b32(bits, 8 * lane + 8, 0, 0);
+        if (LONG) d.w[3] = w.w;
     }
 #pragma unroll
     for (uint32_t r = 0; r < G::kRounds; ++r) {
@@ -329,8 +328,10 @@ __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES,
     using G = Geometry<ES>;
     constexpr uint32_t V = G::V;
     const uint32_t count = lane < ti.n_win ? d.meta >> 8 : 0u;
-    const uint32_t offset = wave_inclusive_scan(count) - count;
-    uint8_t* const first = stage + ti.s0 + offset;
+    // The first window's skipped bytes land in the staging area's prefix
+    // (NZ_STAGE_ORIGIN exceeds any skip, so the index stays positive).
+    const uint32_t at = NZ_STAGE_ORIGIN + ti.s0 + (wave_inclusive_scan(count) - count) - ti.skip;
+    uint8_t* const first = stage + at;
     if (count) {
         uint32_t w0 = bswap32(d.w[0]), w1 = bswap32(d.w[1]), w2 = bswap32(d.w[2]), w3 = LONG ? bswap32(d.w[3]) : 0u;
         {   // restart at the gap
@@ -374,25 +375,26 @@ __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES,
     for (uint32_t r = 0; r < G::kRounds; ++r) {
         const uint32_t g = (lane + NZ_WAVE * r) * V;
         const bool whole = g >= ti.s0 && g + V <= ti.s1;
-        const uint32_t at = whole ? g : 0u;
+        const uint8_t* at = stage + NZ_STAGE_ORIGIN + (whole ? g : 0u);
         uint32_t e0, e1 = 0;
         if (ES == 2) {
-            const uint2 e = *reinterpret_cast<const uint2*>(stage + at);
+            const uint2 e = *reinterpret_cast<const uint2*>(at);
             e0 = e.x;
             e1 = e.y;
         } else {
-            e0 = *reinterpret_cast<const uint32_t*>(stage + at);
+            e0 = *reinterpret_cast<const uint32_t*>(at);
         }
         const uint4 v = merge_vector<ES, REORDER>(e0, e1, d.raw[r]);
         const v4u vv = {v.x, v.y, v.z, v.w};
         __builtin_amdgcn_raw_buffer_store_b128(vv, out, whole ? g * ES : kOutOfRange, 0, 0);
     }
-    {   // elements of the partial first and last vectors
+    if (ti.s0 != 0 || ti.s1 % V != 0) {   // elements of the partial first and last vectors (fragment ends)
         const uint32_t g = edge_index<ES>(ti, lane);
         const uint32_t vec0 = g & ~(V - 1);
         const bool partial = !(vec0 >= ti.s0 && vec0 + V <= ti.s1);
         const bool mine = lane < 2 * V && (lane < V || ti.nv > 1) && partial && g >= ti.s0 && g < ti.s1;
-        store_element<ES, REORDER>(out, mine ? g * ES : kOutOfRange, stage[mine ? g : 0u], d.edge);
+        store_element<ES, REORDER>(out, mine ? g * ES : kOutOfRange, stage[NZ_STAGE_ORIGIN + (mine ? g : 0u)],
+                                   d.edge);
     }
     wave_lds_sync();
 }
@@ -437,104 +439,162 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
     }
 }
 
+// The next tile index of the workgroup's segment for this wavefront (one LDS
+// atomic from lane 0, broadcast). Indices at or past the segment's size mean
+// it is used up.
+__device__ __forceinline__ uint32_t claim(uint32_t* counter, uint32_t lane) {
+    uint32_t v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+// One wavefront's share of a Huffman segment: claim tiles until the segment
+// is used up, fetching (and claiming) one tile ahead of the one it decodes.
 template <int ES, bool REORDER, bool LONG, bool ESC>
-__device__ __forceinline__ void huffman_tiles(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
-                                              const nz_work& wk, uint32_t wave, uint32_t lane, const uint32_t* lut,
-                                              uint8_t* stage, uint8_t* out) {
-    uint32_t t = wk.tile0 + wave;
-    if (t >= wk.tile1) return;
-    TileInfo cur = tile_info<ES>(base, frags, tiles, t, out);
+__device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                                                const nz_work& seg, uint32_t* counter, uint32_t lane,
+                                                const uint32_t* lut, uint8_t* stage, uint8_t* out) {
+    const uint32_t n = seg.tile1 - seg.tile0;
+    uint32_t t = claim(counter, lane);
+    if (t >= n) return;
+    TileInfo cur = tile_info<ES>(base, frags, tiles, seg.tile0 + t, out);
     Fetch<ES, LONG> fc;
     fetch<ES, LONG>(cur, lane, fc);
+    uint32_t tn = claim(counter, lane);
     for (;;) {
-        const uint32_t tn = t + kWaves;
-        const bool more = tn < wk.tile1;
-        const TileInfo nxt = tile_info<ES>(base, frags, tiles, more ? tn : t, out);
+        const bool more = tn < n;
+        const TileInfo nxt = tile_info<ES>(base, frags, tiles, seg.tile0 + (more ? tn : t), out);
         Fetch<ES, LONG> fn;
         fetch<ES, LONG>(nxt, lane, fn);
+        const uint32_t after = more ? claim(counter, lane) : n;
         huffman_tile<ES, REORDER, LONG, ESC>(cur, fc, lut, stage, lane);
         if (!more) break;
         t = tn;
+        tn = after;
         cur = nxt;
         fc = fn;
     }
 }
 
+template <int ES, bool REORDER>
+__device__ __forceinline__ void raw_segment(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                                            const nz_work& seg, uint32_t* counter, uint32_t lane, uint8_t* out) {
+    const uint32_t n = seg.tile1 - seg.tile0;
+    for (uint32_t t = claim(counter, lane); t < n; t = claim(counter, lane)) {
+        const nz_tile tile = tiles[seg.tile0 + t];
+        const nz_frag_desc f = frags[tile.frag];
+        raw_tile<ES, REORDER>(base, f, tile, lane, out);
+    }
+}
+
+// Launch: one workgroup per segment (segments are cut to equal work, about
+// as many as the device runs at once); its wavefronts claim the segment's
+// tiles one at a time, so a wavefront with cheap tiles takes more of them.
 template <int ES, bool REORDER, bool LONG>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NZ_WAVES_PER_EU)))
 void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
-                      const nz_tile* __restrict__ tiles, const nz_work* __restrict__ work,
+                      const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs,
                       uint8_t* __restrict__ out) {
     using G = Geometry<ES>;
     __shared__ __align__(16) uint32_t s_lut[NZ_LUT_MAX_WORDS];
     __shared__ __align__(16) uint8_t s_stage[kWaves][G::kStage];
-    const nz_work wk = work[blockIdx.x];
+    __shared__ uint32_t s_claim;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / NZ_WAVE);
     const uint32_t lane = threadIdx.x % NZ_WAVE;
-    if (wk.kind == NZ_KIND_RAW) {
-        for (uint32_t t = wk.tile0 + wave; t < wk.tile1; t += kWaves) {
-            const nz_tile tile = tiles[t];
-            const nz_frag_desc f = frags[tile.frag];
-            raw_tile<ES, REORDER>(base, f, tile, lane, out);
-        }
+    const nz_work seg = segs[blockIdx.x];
+    if (threadIdx.x == 0) s_claim = 0;
+    if (seg.kind == NZ_KIND_RAW) {
+        __syncthreads();
+        raw_segment<ES, REORDER>(base, frags, tiles, seg, &s_claim, lane, out);
         return;
     }
-    const uint4* img = reinterpret_cast<const uint4*>(base + frags[wk.lut_frag].lut);
-    const uint32_t escapes = reinterpret_cast<const uint32_t*>(img)[0];
-    {
-        const uint32_t words = reinterpret_cast<const uint32_t*>(img)[2];
-        uint4* dst = reinterpret_cast<uint4*>(s_lut);
-        for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kThreads) dst[i] = img[i];
-        __syncthreads();
-    }
+    const uint4* img = reinterpret_cast<const uint4*>(base + frags[seg.lut_frag].lut);
+    const uint32_t words = reinterpret_cast<const uint32_t*>(img)[2];
+    uint4* dst = reinterpret_cast<uint4*>(s_lut);
+    for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kThreads) dst[i] = img[i];
+    __syncthreads();
     // Codebooks whose codes all fit the primary table run the loop without
     // the escape check (long-code codebooks always have escapes).
     if constexpr (LONG) {
-        huffman_tiles<ES, REORDER, true, true>(base, frags, tiles, wk, wave, lane, s_lut, s_stage[wave], out);
+        huffman_segment<ES, REORDER, true, true>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave], out);
     } else {
-        if (escapes)
-            huffman_tiles<ES, REORDER, false, true>(base, frags, tiles, wk, wave, lane, s_lut, s_stage[wave], out);
+        if (s_lut[0])
+            huffman_segment<ES, REORDER, false, true>(base, frags, tiles, seg, &s_claim, lane, s_lut,
+                                                      s_stage[wave], out);
         else
-            huffman_tiles<ES, REORDER, false, false>(base, frags, tiles, wk, wave, lane, s_lut, s_stage[wave], out);
+            huffman_segment<ES, REORDER, false, false>(base, frags, tiles, seg, &s_claim, lane, s_lut,
+                                                       s_stage[wave], out);
     }
 }
 
 template <int ES, bool REORDER, bool LONG>
-hipError_t launch(const void* base, const void* frags, const void* tiles, const void* work, uint32_t n_work,
+hipError_t launch(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
                   void* out, hipStream_t stream) {
-    hipLaunchKernelGGL((nz_decode_kernel<ES, REORDER, LONG>), dim3(n_work), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((nz_decode_kernel<ES, REORDER, LONG>), dim3(n_segs), dim3(kThreads), 0, stream,
                        static_cast<const uint8_t*>(base), static_cast<const nz_frag_desc*>(frags),
-                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(work),
+                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs),
                        static_cast<uint8_t*>(out));
     return hipGetLastError();
 }
 
+template <int ES, bool REORDER, bool LONG>
+hipError_t slots(int* out) {
+    int device = 0, cus = 0, per_cu = 0;
+    hipError_t rc = hipGetDevice(&device);
+    if (rc == hipSuccess) rc = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (rc == hipSuccess)
+        rc = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nz_decode_kernel<ES, REORDER, LONG>, kThreads, 0);
+    *out = cus * per_cu;
+    return rc;
+}
+
 }  // namespace
 
-// Launch one decode over `n_work` workgroups on `stream` (stream-ordered,
-// asynchronous). Returns 0 or a negative error code.
-extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* work,
-                                    uint32_t n_work, int element_size, int bit_reorder, int long_codes,
-                                    void* out, void* stream, char* message, size_t message_size) {
-    if (n_work == 0) return 0;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+// Launch one decode of `n_segs` segments (one workgroup each) on `stream`
+// (stream-ordered, asynchronous). Returns 0 or a negative error code.
+extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* segs,
+                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes, void* out,
+                                    void* stream, char* message, size_t message_size) {
+    if (n_segs == 0) return 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t rc;
+#define NZ_LAUNCH(E, R, L) launch<E, R, L>(base, frags, tiles, segs, n_segs, out, st)
+    if (element_size == 2 && bit_reorder)
+        rc = long_codes ? NZ_LAUNCH(2, true, true) : NZ_LAUNCH(2, true, false);
+    else if (element_size == 2)
+        rc = long_codes ? NZ_LAUNCH(2, false, true) : NZ_LAUNCH(2, false, false);
+    else if (element_size == 4 && bit_reorder)
+        rc = long_codes ? NZ_LAUNCH(4, true, true) : NZ_LAUNCH(4, true, false);
+    else {
+        snprintf(message, message_size, "Unsupported GPU layout (element_size=%d, bit_reorder=%d).",
+                 element_size, bit_reorder);
+        return -1;
+    }
+#undef NZ_LAUNCH
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "decode launch failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    return 0;
+}
+
+// Workgroups of the decode kernel the current device runs at once.
+extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_codes, int* out, char* message,
+                                   size_t message_size) {
     hipError_t rc;
     if (element_size == 2 && bit_reorder)
-        rc = long_codes ? launch<2, true, true>(base, frags, tiles, work, n_work, out, s)
-                        : launch<2, true, false>(base, frags, tiles, work, n_work, out, s);
+        rc = long_codes ? slots<2, true, true>(out) : slots<2, true, false>(out);
     else if (element_size == 2)
-        rc = long_codes ? launch<2, false, true>(base, frags, tiles, work, n_work, out, s)
-                        : launch<2, false, false>(base, frags, tiles, work, n_work, out, s);
+        rc = long_codes ? slots<2, false, true>(out) : slots<2, false, false>(out);
     else if (element_size == 4 && bit_reorder)
-        rc = long_codes ? launch<4, true, true>(base, frags, tiles, work, n_work, out, s)
-                        : launch<4, true, false>(base, frags, tiles, work, n_work, out, s);
+        rc = long_codes ? slots<4, true, true>(out) : slots<4, true, false>(out);
     else {
         snprintf(message, message_size, "Unsupported GPU layout (element_size=%d, bit_reorder=%d).",
                  element_size, bit_reorder);
         return -1;
     }
     if (rc != hipSuccess) {
-        snprintf(message, message_size, "decode launch failed: %s", hipGetErrorString(rc));
+        snprintf(message, message_size, "decode occupancy query failed: %s", hipGetErrorString(rc));
         return -6;
     }
     return 0;

@@ -153,22 +153,31 @@ Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const
     }
     if (total < numel) fail(kCorruptStream, "Layout simulation emitted fewer bytes than elements.");
     // Group windows into wavefront tiles. Only trailing windows can be empty:
-    // the previous window's last step may overrun the final code into the
-    // zero padding, past the start of the last window's range.
+    // the previous window's last multi-token step may overrun the final code
+    // into the zero padding, past the start of the last window's range.
     uint64_t used_windows = n_windows;
     while (used_windows > 0 && counts[used_windows - 1] == 0) --used_windows;
+    std::vector<uint64_t> cum(used_windows + 1, 0);   // bytes emitted before each window
+    for (uint64_t w = 0; w < used_windows; ++w) cum[w + 1] = cum[w] + counts[w];
     const uint64_t capacity = nz_tile_capacity(static_cast<int>(es));
-    uint64_t out0 = 0;
-    for (uint64_t w = 0; w < used_windows;) {
-        uint64_t end = w, sum = 0;
-        while (end < used_windows && end - w < NZ_WAVE && sum + counts[end] <= capacity) sum += counts[end++];
-        if (end == w) fail(kLayoutLimit, "A window exceeds the tile staging capacity.");
-        const uint64_t n_out = std::min<uint64_t>(sum, numel - std::min<uint64_t>(out0, numel));
-        if (n_out == 0) fail(kCorruptStream, "Empty tile in layout.");
-        f.tiles.push_back({0, static_cast<uint32_t>(w), static_cast<uint32_t>(out0),
-                           static_cast<uint32_t>((end - w) | (n_out << 16))});
-        out0 += sum;
-        w = end;
+    uint64_t a0 = 0, w0 = 0;
+    while (a0 < numel) {
+        while (cum[w0 + 1] <= a0) ++w0;              // the window holding element a0
+        const uint64_t skip = a0 - cum[w0];
+        const uint64_t s0 = (out + a0) % V;
+        const uint64_t w_end = std::min<uint64_t>(w0 + NZ_WAVE, used_windows);
+        const uint64_t limit = std::min<uint64_t>(numel, std::min<uint64_t>(cum[w_end], a0 + capacity - s0));
+        uint64_t a1 = limit;
+        if (limit < numel) {   // end on a line boundary of the workspace when the tile allows it
+            const uint64_t aligned = (out + limit) / NZ_TILE_ALIGN * NZ_TILE_ALIGN;
+            if (aligned > out + a0) a1 = aligned - out;
+        }
+        uint64_t w1 = w0;
+        while (cum[w1 + 1] < a1) ++w1;               // the window holding element a1 - 1
+        f.tiles.push_back({0, static_cast<uint32_t>(w0), static_cast<uint32_t>(a0),
+                           nz_tile_counts(static_cast<uint32_t>(w1 - w0 + 1), static_cast<uint32_t>(skip),
+                                          static_cast<uint32_t>(a1 - a0))});
+        a0 = a1;
     }
     return f;
 }
@@ -198,24 +207,68 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
     d->reserved = 0;
 }
 
-std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
-                               uint32_t target_groups) {
-    std::vector<nz_work> work;
-    if (!n_tiles) return work;
-    const uint32_t per = std::max<uint32_t>(1, (n_tiles + std::max<uint32_t>(target_groups, 1) - 1) /
-                                                   std::max<uint32_t>(target_groups, 1));
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
+    std::vector<nz_work> runs;   // maximal runs of one LUT and kind
+    if (!n_tiles) return runs;
     auto key = [&](uint32_t t) {
         const nz_frag_desc& f = frags[tiles[t].frag];
         return std::pair<uint64_t, uint32_t>(f.kind == NZ_KIND_RAW ? 0 : f.lut, f.kind);
     };
+    std::vector<double> cost;
     uint32_t start = 0;
-    for (uint32_t t = 1; t <= n_tiles; ++t) {
-        if (t == n_tiles || t - start >= per || key(t) != key(start)) {
-            work.push_back({start, t, tiles[start].frag, frags[tiles[start].frag].kind});
+    double sum = 0;
+    for (uint32_t t = 0; t <= n_tiles; ++t) {
+        if (t == n_tiles || key(t) != key(start)) {
+            runs.push_back({start, t, tiles[start].frag, frags[tiles[start].frag].kind});
+            cost.push_back(sum);
             start = t;
+            sum = 0;
+        }
+        if (t < n_tiles) {   // raw tiles only copy and merge: count them at half weight
+            const double n = nz_tile_elements(tiles[t].counts);
+            sum += frags[tiles[t].frag].kind == NZ_KIND_RAW ? 0.5 * n : n;
         }
     }
-    return work;
+    const size_t n_seg = runs.size();
+    const uint64_t groups = std::max<uint64_t>(slots, n_seg);
+    std::vector<uint64_t> share(n_seg, 1);
+    double total = 0;
+    for (double c : cost) total += c;
+    if (groups > n_seg && total > 0) {
+        // largest remainder over the workgroups left after one per segment
+        const uint64_t extra = groups - n_seg;
+        std::vector<std::pair<double, size_t>> rest;
+        uint64_t given = 0;
+        for (size_t i = 0; i < n_seg; ++i) {
+            const double exact = extra * cost[i] / total;
+            const uint64_t whole = static_cast<uint64_t>(exact);
+            share[i] += whole;
+            given += whole;
+            rest.push_back({exact - whole, i});
+        }
+        std::sort(rest.begin(), rest.end(), [](auto& x, auto& y) { return x.first > y.first || (x.first == y.first && x.second < y.second); });
+        for (size_t k = 0; given < extra; ++k, ++given) share[rest[k % n_seg].second] += 1;
+    }
+    // Cut each run into its share of ranges of about equal cost.
+    std::vector<nz_work> ranges;
+    for (size_t i = 0; i < n_seg; ++i) {
+        const nz_work& run = runs[i];
+        const uint64_t parts = std::min<uint64_t>(share[i], run.tile1 - run.tile0);
+        double acc = 0;
+        uint32_t begin = run.tile0;
+        uint64_t made = 0;
+        for (uint32_t t = run.tile0; t < run.tile1; ++t) {
+            const double n = nz_tile_elements(tiles[t].counts);
+            acc += frags[tiles[t].frag].kind == NZ_KIND_RAW ? 0.5 * n : n;
+            const bool last = t + 1 == run.tile1;
+            if (last || (made + 1 < parts && acc >= cost[i] * (made + 1) / parts && run.tile1 - (t + 1) >= parts - made - 1)) {
+                ranges.push_back({begin, t + 1, tiles[begin].frag, run.kind});
+                begin = t + 1;
+                ++made;
+            }
+        }
+    }
+    return ranges;
 }
 
 namespace {
@@ -237,8 +290,10 @@ uint32_t lane_bytes(const uint8_t* base, const nz_frag_desc& f, uint64_t g, unsi
 
 void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
                     const nz_work* work, uint32_t n_work, unsigned es, bool reorder, uint8_t* out) {
+    // Every tile of every segment, in order: the kernel's claim order only
+    // changes which wavefront decodes a tile, not what it writes.
     const uint64_t V = nz_vector_elements(static_cast<int>(es));
-    std::vector<uint8_t> stage(nz_tile_capacity(static_cast<int>(es)) + 32);
+    std::vector<uint8_t> stage(NZ_STAGE_ORIGIN + nz_tile_capacity(static_cast<int>(es)) + NZ_STAGE_SLACK);
     for (uint32_t wi = 0; wi < n_work; ++wi) {
         // the workgroup stages the LUT of work[wi].lut_frag
         const nz_frag_desc& lf = frags[work[wi].lut_frag];
@@ -265,6 +320,7 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
             for (unsigned l = 1; l < n_win; ++l)
                 offset[l] = offset[l - 1] + (base[f.meta + 2 * (tile.win0 + l - 1) + 1]);
             const uint64_t s0 = A0 - A0 / V * V;
+            const uint64_t origin = NZ_STAGE_ORIGIN + s0 - nz_tile_skip(tile.counts);
             std::fill(stage.begin(), stage.end(), 0xA5);
             for (unsigned l = 0; l < n_win; ++l) {
                 const uint64_t w = tile.win0 + l;
@@ -285,7 +341,7 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
                 };
                 shift(gap);
                 uint64_t pos = gap;
-                uint64_t o = s0 + offset[l];
+                uint64_t o = origin + offset[l];
                 while (pos < end) {
                     const uint64_t window = (static_cast<uint64_t>(hi) << 32) | mid;
                     uint32_t bytes;
@@ -298,7 +354,7 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
                 }
             }
             for (uint64_t g = A0; g < A1; ++g)
-                put_element(out, g, es, reorder, lane_bytes(base, f, g, es, stage[g - A0 / V * V]));
+                put_element(out, g, es, reorder, lane_bytes(base, f, g, es, stage[NZ_STAGE_ORIGIN + g - A0 / V * V]));
         }
     }
 }

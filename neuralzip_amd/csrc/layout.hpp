@@ -50,15 +50,17 @@ uint64_t packed_size(const Fragment& f);
 void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lut_offset,
                    nz_frag_desc* desc);
 
-// Splits `n_tiles` tiles into workgroup ranges that never mix fragments of
-// different LUTs or kinds.
-std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
-                               uint32_t target_groups);
+// Launch plan over `n_tiles` tiles (callers order them so that tiles of one
+// LUT and kind are adjacent): one segment per workgroup. Maximal runs of one
+// LUT and kind share out `slots` workgroups (the number the device runs at
+// once; at least one per run) in proportion to their elements, and each run
+// is cut into that many contiguous segments of about equal elements.
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots);
 
 // CPU emulation of the decode kernel over a packed buffer; writes words
 // into `out` (the output workspace image).
 void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
-                    const nz_work* work, uint32_t n_work, unsigned element_size, bool reorder,
+                    const nz_work* segments, uint32_t n_segments, unsigned element_size, bool reorder,
                     uint8_t* out);
 
 }  // namespace nz

@@ -16,10 +16,14 @@
 // own step sequence, which replaces the reference's count pass
 // (decode.cu:198-222) and its 4/8-bit restart gaps (gpu_layout.h:128-183).
 //
-// Tiles. A tile is up to 64 consecutive windows (one wavefront) whose counts
-// sum to at most NZ_TILE_OUT bytes; the wavefront turns counts into output
-// positions with a ballot prefix scan, stages the exponent bytes in LDS and
-// writes merged words with 16-byte stores.
+// Tiles. A tile is up to 64 consecutive windows (one wavefront) and a range
+// of at most NZ_TILE_OUT output elements that ends on a multiple of
+// NZ_TILE_ALIGN elements of the output workspace (except at the fragment's
+// end), so that tiles write whole 128-byte lines. A window that straddles
+// two tiles is decoded by both: the later tile skips the window's first
+// `skip` bytes. The wavefront turns counts into output positions with a
+// prefix scan, stages the exponent bytes in LDS and writes merged words with
+// 16-byte stores.
 #pragma once
 #include <stdint.h>
 
@@ -34,6 +38,9 @@
 #define NZ_TILE_OUT 2048          // max exponent bytes staged per tile (16-bit words)
 #define NZ_TILE_OUT32 1024        // the same for 32-bit words
 #define NZ_RAW_TILE 2048          // elements per tile of a raw fragment
+#define NZ_TILE_ALIGN 64          // Huffman tiles end on multiples of this many output elements
+#define NZ_STAGE_ORIGIN 256       // staging bytes ahead of a tile's first element (skipped bytes land there)
+#define NZ_STAGE_SLACK 272        // staging bytes after the tile (the last window's excess, store spill)
 #define NZ_LUT_BITS 12
 #define NZ_LUT_ENTRIES (1 << NZ_LUT_BITS)
 #define NZ_BITS_PAD 16            // zero bytes after each bitstream
@@ -79,16 +86,25 @@ struct nz_tile {                 // 16 bytes, one wavefront's work
     uint32_t frag;
     uint32_t win0;               // first window (Huffman fragments)
     uint32_t out0;               // first element, relative to the fragment
-    uint32_t counts;             // windows (Huffman fragments) | elements << 16
+    uint32_t counts;             // windows | skipped bytes << 7 | elements << 16
 };
 
-NZ_HD static inline uint32_t nz_tile_windows(uint32_t counts) { return counts & 0xFFFFu; }
+NZ_HD static inline uint32_t nz_tile_windows(uint32_t counts) { return counts & 0x7Fu; }
+NZ_HD static inline uint32_t nz_tile_skip(uint32_t counts) { return (counts >> 7) & 0xFFu; }
 NZ_HD static inline uint32_t nz_tile_elements(uint32_t counts) { return counts >> 16; }
+NZ_HD static inline uint32_t nz_tile_counts(uint32_t windows, uint32_t skip, uint32_t elements) {
+    return windows | (skip << 7) | (elements << 16);
+}
 NZ_HD static inline uint32_t nz_tile_capacity(int element_size) { return element_size == 4 ? NZ_TILE_OUT32 : NZ_TILE_OUT; }
 
-struct nz_work {                 // 16 bytes, one workgroup's contiguous tile range
+// A *segment*: a contiguous range of tiles sharing one LUT and kind, the
+// work of one workgroup. A launch has about as many segments, of about equal
+// elements, as the device runs workgroups at once; the wavefronts of a
+// workgroup claim the segment's tiles one at a time (an LDS counter), so the
+// work evens out between them.
+struct nz_work {                 // 16 bytes, one segment
     uint32_t tile0, tile1;
-    uint32_t lut_frag;           // fragment whose LUT the workgroup stages
+    uint32_t lut_frag;           // fragment whose LUT the segment's workgroups stage
     uint32_t kind;
 };
 

@@ -16,9 +16,10 @@ from neuralzip_amd._native import FRAG_DESC, KIND_LONG, KIND_RAW, TILE
 
 THREADS_PER_BLOCK = 256
 WINDOW_BITS = 64
-# Workgroups per launch the work planner aims at: four per CU on 256 CUs
-# (two 16-wavefront workgroups fit a CU at a time).
-TARGET_GROUPS = 1024
+# Workgroups per launch: None asks the device how many decode workgroups it
+# runs at once (two 16-wavefront workgroups per CU on MI355X, 512 in all), so
+# that one round of equal-work workgroups covers the launch.
+SLOTS = None
 
 
 def _align(value, alignment=256):
@@ -85,11 +86,13 @@ class DeviceStore:
 
 @dataclass(frozen=True)
 class PreparedBatch:
-    """One launch: the workgroup plan over the tiles of some fragments."""
-    descriptor_tensors: tuple = field(repr=False)      # (tiles, work) on the device
+    """One launch: the tiles of some fragments, cut into segments of one LUT
+    (one workgroup each)."""
+    descriptor_tensors: tuple = field(repr=False)      # (tiles, segments) on the device
     device: torch.device
     layout: tuple                                      # (element_size, bit_reorder, long_codes)
     kernel_grid: tuple
+    n_segments: int
     store: DeviceStore = field(repr=False)
     output: torch.Tensor = field(repr=False)
     outputs: tuple = field(repr=False, default=())
@@ -115,8 +118,9 @@ class HIPDecoder:
         _native.lib()
         return group.layout
 
-    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), target_groups=TARGET_GROUPS):
-        """Tiles of `fragment_indices` (one dtype and kind) and their workgroup plan."""
+    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), slots=SLOTS):
+        """Tiles of `fragment_indices` (one dtype and kind), ordered so that
+        fragments of one LUT are adjacent, and their launch plan."""
         fragment_indices = list(fragment_indices)
         if not fragment_indices:
             raise ValueError("A decode batch must contain at least one group.")
@@ -124,21 +128,33 @@ class HIPDecoder:
         if len(keys) > 1:
             raise ValueError("A decode batch must use one layout.")
         key = keys.pop() if keys else (dtype.element_size, bool(dtype.bit_reorder), False)
-        tiles = np.concatenate([store.fragment_tiles(i) for i in fragment_indices])
-        work = _native.plan_work(store.descs, tiles, target_groups)
+        order = sorted(fragment_indices, key=lambda i: (int(store.descs[i]["kind"]), int(store.descs[i]["lut"]), i))
+        tiles = np.concatenate([store.fragment_tiles(i) for i in order])
         device = store.device
+        if slots is None:
+            slots = self.slots(device, key)
+        segments = _native.plan_work(store.descs, tiles, slots)
         tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
-        work_t = torch.from_numpy(work.view(np.uint8).copy()).to(device)
-        return PreparedBatch((tiles_t, work_t), device, key, (len(work),), store, output, tuple(outputs),
-                             algorithmic_bytes(store.descs[fragment_indices], dtype))
+        segments_t = torch.from_numpy(segments.view(np.uint8).copy()).to(device)
+        return PreparedBatch((tiles_t, segments_t), device, key, (len(segments),), len(segments), store, output,
+                             tuple(outputs), algorithmic_bytes(store.descs[fragment_indices], dtype))
+
+    def slots(self, device, key):
+        """Decode workgroups `device` runs at once for layout `key` (cached)."""
+        cache = self.__dict__.setdefault("_slots", {})
+        device = torch.device(device)
+        if (device, key) not in cache:
+            with torch.cuda.device(device):
+                cache[(device, key)] = _native.decode_slots(*key)
+        return cache[(device, key)]
 
     def decode_batch(self, prepared, stream=None):
         if stream is None:
             stream = torch.cuda.current_stream(prepared.device)
-        tiles_t, work_t = prepared.descriptor_tensors
+        tiles_t, segments_t = prepared.descriptor_tensors
         element_size, bit_reorder, long_codes = prepared.layout
         _native.decode_launch(prepared.store.buffer.data_ptr(), prepared.store.frags.data_ptr(),
-                              tiles_t.data_ptr(), work_t.data_ptr(), prepared.kernel_grid[0], element_size,
+                              tiles_t.data_ptr(), segments_t.data_ptr(), prepared.n_segments, element_size,
                               bit_reorder, long_codes, prepared.output.data_ptr(), stream.cuda_stream)
         return prepared.outputs
 

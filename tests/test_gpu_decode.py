@@ -16,39 +16,52 @@ from nz_helpers import Encoded, segment_lengths, segment_tensor, singleton_heade
 pytestmark = pytest.mark.gpu
 
 
-def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, target_groups=2048):
+def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, slots=None, launches=2):
+    """Decodes every tile (one launch per kind) `launches` times in a row,
+    poisoning the workspace before each round; returns the workspace bytes
+    of every round and the plans."""
     device = torch.device("cuda:0")
-    work_all = _native.plan_work(descs, tiles, target_groups)
     out = torch.full((workspace_elements * element_size + 64,), 0xA5, dtype=torch.uint8, device=device)
     base_t = torch.from_numpy(base).to(device)
     frags_t = torch.from_numpy(descs.view(np.uint8).copy()).to(device)
-    tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
     stream = torch.cuda.current_stream(device)
+    kinds = descs["kind"][tiles["frag"]]
+    plans = []
     for long_codes in (0, 1):
-        sel = [w for w in work_all if (w["kind"] == _native.KIND_LONG) == bool(long_codes)]
-        if not sel:
+        sel = tiles[(kinds == _native.KIND_LONG) == bool(long_codes)]
+        if not len(sel):
             continue
-        work_t = torch.from_numpy(np.array(sel, dtype=_native.WORK).view(np.uint8).copy()).to(device)
-        _native.decode_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), work_t.data_ptr(),
-                              len(sel), element_size, bit_reorder, long_codes, out.data_ptr(),
-                              stream.cuda_stream)
-    torch.cuda.synchronize(device)
-    return out.cpu().numpy(), work_all
+        n = slots if slots is not None else _native.decode_slots(element_size, bit_reorder, long_codes)
+        segments = _native.plan_work(descs, sel, n)
+        plans.append((long_codes, sel, segments,
+                      [torch.from_numpy(a.view(np.uint8).copy()).to(device) for a in (sel, segments)]))
+    rounds = []
+    for _ in range(launches):
+        out.fill_(0xA5)
+        for long_codes, sel, segments, (tiles_t, segments_t) in plans:
+            _native.decode_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), segments_t.data_ptr(),
+                                  len(segments), element_size, bit_reorder, long_codes, out.data_ptr(),
+                                  stream.cuda_stream)
+        torch.cuda.synchronize(device)
+        rounds.append(out.cpu().numpy())
+    return rounds, plans
 
 
-def check_case(tensors, codebooks, dtype, repeats=2, target_groups=2048):
+def check_case(tensors, codebooks, dtype, repeats=1, slots=None):
     spec = DTYPES[dtype]
     enc = Encoded(tensors, codebooks)
     base, descs, tiles = enc.host_image()
     size = max(off + raw.size // spec.element_size for raw, _, _, _, off in tensors)
     for _ in range(repeats):
-        got, work = run_gpu(base, descs, tiles, spec.element_size, spec.bit_reorder, size, target_groups)
-        emu = np.full_like(got, 0xA5)
-        _native.emulate_decode(base, descs, tiles, work, spec.element_size, spec.bit_reorder, emu)
-        for raw, _, _, _, off in tensors:
-            lo = off * spec.element_size
-            assert np.array_equal(got[lo:lo + raw.size], raw)
-        assert np.array_equal(got, emu)
+        rounds, plans = run_gpu(base, descs, tiles, spec.element_size, spec.bit_reorder, size, slots)
+        emu = np.full_like(rounds[0], 0xA5)
+        for _, sel, segments, _ in plans:
+            _native.emulate_decode(base, descs, sel, segments, spec.element_size, spec.bit_reorder, emu)
+        for got in rounds:
+            for raw, _, _, _, off in tensors:
+                lo = off * spec.element_size
+                assert np.array_equal(got[lo:lo + raw.size], raw)
+            assert np.array_equal(got, emu)
 
 
 def test_config1_shape_singleton_bf16():
@@ -100,11 +113,11 @@ def test_long_codes_from_skewed_counts():
     check_case([(raw, torch.bfloat16, 1 << 20, [0], 0)], {0: book}, torch.bfloat16)
 
 
-@pytest.mark.parametrize("target_groups", [1, 7, 100000])
-def test_work_partitions_give_identical_output(target_groups):
+@pytest.mark.parametrize("slots", [1, 7, 100000])
+def test_work_partitions_give_identical_output(slots):
     g = torch.Generator().manual_seed(3)
     raw = (torch.randn(1000, 1000, generator=g) * 0.05).bfloat16().view(torch.uint8).numpy().reshape(-1)
     books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16)),
              1: _native.Codebook(singleton_header(raw[: 20000], torch.bfloat16, prior=3))}
     ids = [(0, 1, -1)[j % 3] for j in range(-(-1000000 // 65536))]
-    check_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, target_groups=target_groups)
+    check_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, slots=slots)

@@ -15,15 +15,20 @@ from neuralzip_amd.dtypes import DTYPES
 from nz_helpers import Encoded, segment_lengths, segment_tensor, singleton_header
 
 
-def emulate_case(tensors, codebooks, dtype, target_groups=2048):
+def emulate_case(tensors, codebooks, dtype, slots=512):
     spec = DTYPES[dtype]
     base, descs, tiles = Encoded(tensors, codebooks).host_image()
     size = max(off + raw.size // spec.element_size for raw, _, _, _, off in tensors)
     out = np.full(size * spec.element_size + 64, 0xA5, dtype=np.uint8)
-    work = _native.plan_work(descs, tiles, target_groups)
-    assert work["tile1"][-1] == len(tiles) and work["tile0"][0] == 0
-    assert np.all(work["tile0"][1:] == work["tile1"][:-1])
-    _native.emulate_decode(base, descs, tiles, work, spec.element_size, spec.bit_reorder, out)
+    segments = _native.plan_work(descs, tiles, slots)
+    # segments tile the tile array
+    assert segments["tile1"][-1] == len(tiles) and segments["tile0"][0] == 0
+    assert np.all(segments["tile0"][1:] == segments["tile1"][:-1])
+    for s in segments:   # one LUT and kind per segment
+        members = descs[tiles["frag"][s["tile0"]:s["tile1"]]]
+        assert len(set(members["kind"])) == 1
+        assert members["kind"][0] == _native.KIND_RAW or len(set(members["lut"])) == 1
+    _native.emulate_decode(base, descs, tiles, segments, spec.element_size, spec.bit_reorder, out)
     for raw, _, _, _, off in tensors:
         lo = off * spec.element_size
         assert np.array_equal(out[lo:lo + raw.size], raw)
@@ -68,14 +73,14 @@ def test_long_codes_from_skewed_counts():
                  torch.bfloat16)
 
 
-@pytest.mark.parametrize("target_groups", [1, 7, 100000])
-def test_work_partitions(target_groups):
+@pytest.mark.parametrize("slots", [1, 7, 100000])
+def test_work_partitions(slots):
     g = torch.Generator().manual_seed(3)
     raw = (torch.randn(300, 1000, generator=g) * 0.05).bfloat16().view(torch.uint8).numpy().reshape(-1)
     books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16)),
              1: _native.Codebook(singleton_header(raw[:20000], torch.bfloat16, prior=3))}
     ids = [(0, 1, -1)[j % 3] for j in range(-(-300000 // 65536))]
-    emulate_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, target_groups)
+    emulate_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, slots)
 
 
 def test_codebook_lengths_match_the_oracle_on_golden_headers():
@@ -123,12 +128,65 @@ def test_trailing_window_without_steps():
         symbols = rng.choice([0, 1, 2], int(rng.integers(20, 300))).astype(np.uint8)
         raw = segment_tensor(torch.bfloat16, symbols)
         layout = _native.Layout([(raw, book, 0, spec)])
-        found |= sum(_tiles_windows(layout)) < layout.info(0)["n_windows"]
+        found |= _windows_covered(layout) < layout.info(0)["n_windows"]
         emulate_case([(raw, torch.bfloat16, 1 << 20, [0], 0)], {0: book}, torch.bfloat16)
     assert found, "no trailing empty window was produced"
 
 
-def _tiles_windows(layout):
+def _windows_covered(layout):
     base = np.zeros(layout.packed_bytes + 64, dtype=np.uint8)
     _, tiles = layout.pack(base, 0, np.zeros(1, np.uint64))
-    return [int(t["n_win"]) for t in tiles]
+    return int((tiles["win0"] + _native.tile_windows(tiles)).max())
+
+
+@pytest.mark.parametrize("dtype,out", [(torch.bfloat16, 0), (torch.bfloat16, 37), (torch.float32, 5),
+                                       (torch.float16, 128)])
+def test_tiles_end_on_lines(dtype, out):
+    """Huffman tiles cover the fragment in order, end on 64-element lines of
+    the workspace (the fragment's end aside), fit the staging capacity, and
+    start inside their first window (skip < that window's count)."""
+    spec = DTYPES[dtype]
+    g = torch.Generator().manual_seed(11)
+    t = (torch.randn(300001, generator=g) * 0.03).to(dtype)
+    raw = t.view(torch.uint8).numpy().reshape(-1)
+    book = _native.Codebook(singleton_header(raw, dtype))
+    layout = _native.Layout([(raw, book, out, spec)])
+    base = np.zeros(layout.packed_bytes + 64, dtype=np.uint8)
+    descs, tiles = layout.pack(base, 0, np.zeros(1, np.uint64))
+    meta = base[descs["meta"][0]:descs["meta"][0] + 2 * layout.info(0)["n_windows"]].view("<u2")
+    counts = (meta >> 8).astype(np.int64)
+    cum = np.concatenate([[0], np.cumsum(counts)])
+    assert tiles["out0"][0] == 0 and np.all(tiles["out0"][1:] == tiles["out0"][:-1] + tiles["n_out"][:-1])
+    assert int(tiles["out0"][-1]) + int(tiles["n_out"][-1]) == t.numel()
+    ends = out + tiles["out0"].astype(np.int64) + tiles["n_out"]
+    assert np.all(ends[:-1] % 64 == 0)
+    windows, skip = _native.tile_windows(tiles), _native.tile_skip(tiles)
+    assert windows.max() <= 64 and windows.min() >= 1
+    cap = 1024 if spec.element_size == 4 else 2048
+    V = 16 // spec.element_size
+    assert np.all((out + tiles["out0"]) % V + tiles["n_out"] <= cap)
+    w0 = tiles["win0"].astype(np.int64)
+    assert np.all(cum[w0] + skip == tiles["out0"]) and np.all(skip < counts[w0])
+    last = w0 + windows - 1   # the last window holds the tile's last element
+    assert np.all(cum[last] < tiles["out0"] + tiles["n_out"])
+    assert np.all(cum[last + 1] >= tiles["out0"] + tiles["n_out"])
+
+
+def test_plan_shares_workgroups_by_elements():
+    descs = np.zeros(3, dtype=_native.FRAG_DESC)
+    descs["kind"] = [_native.KIND_SHORT, _native.KIND_SHORT, _native.KIND_RAW]
+    descs["lut"] = [0, 4096, 0]
+    tiles = np.zeros(6, dtype=_native.TILE)
+    tiles["frag"] = [0, 0, 0, 1, 2, 2]
+    tiles["n_out"] = [1000, 1000, 1000, 1000, 2000, 2000]   # raw tiles count half
+    # runs of 3000, 1000 and 2000 (raw at half) elements; 5 slots: one each,
+    # then 2 more split 1.0 : 0.33 : 0.67 -> the first and the raw run
+    segments = _native.plan_work(descs, tiles, 5)
+    assert segments[["tile0", "tile1"]].tolist() == [(0, 2), (2, 3), (3, 4), (4, 5), (5, 6)]
+    assert segments["kind"].tolist() == [_native.KIND_SHORT] * 3 + [_native.KIND_RAW] * 2
+    # a run is never cut into more segments than it has tiles
+    segments = _native.plan_work(descs, tiles, 100)
+    assert segments[["tile0", "tile1"]].tolist() == [(0, 1), (1, 2), (2, 3), (3, 4), (4, 5), (5, 6)]
+    # fewer slots than runs: one workgroup per run
+    segments = _native.plan_work(descs, tiles, 1)
+    assert segments[["tile0", "tile1"]].tolist() == [(0, 3), (3, 4), (4, 6)]
