@@ -57,6 +57,9 @@ __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
 // selects 32-bit raw data, the untyped layout of the gfx9 family.
 constexpr uint32_t kRawBufferFlags = 0x00020000u;
 constexpr uint32_t kOutOfRange = 0x80000000u;
+// Cache-policy operand of buffer stores: streaming (nontemporal) writes of
+// the decoded words, which the caches need not keep.
+constexpr int kNonTemporal = 2;
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
@@ -386,7 +389,7 @@ __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES,
         }
         const uint4 v = merge_vector<ES, REORDER>(e0, e1, d.raw[r]);
         const v4u vv = {v.x, v.y, v.z, v.w};
-        __builtin_amdgcn_raw_buffer_store_b128(vv, out, whole ? g * ES : kOutOfRange, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(vv, out, whole ? g * ES : kOutOfRange, 0, kNonTemporal);
     }
     if (ti.s0 != 0 || ti.s1 % V != 0) {   // elements of the partial first and last vectors (fragment ends)
         const uint32_t g = edge_index<ES>(ti, lane);
