@@ -115,6 +115,134 @@ def copy_bandwidth(device, nbytes=1 << 30, repeats=10):
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
+LLAMA3_8B = dict(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
+                 num_key_value_heads=8, vocab_size=128256, max_position_embeddings=8192, rope_theta=500000.0,
+                 tie_word_embeddings=False)
+
+
+def random_llama(device, seed=1):
+    """Llama-3-8B-shaped model with bf16 random weights: linears and
+    embeddings N(0, 0.02^2) with 0.1 % of entries replaced by
+    0.02 * Student-t(3), norms 1 (config 4 of the survey)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    config = LlamaConfig(**LLAMA3_8B, torch_dtype=torch.bfloat16)
+    with torch.device("meta"):
+        model = LlamaForCausalLM(config)
+    model = model.to_empty(device=device).to(torch.bfloat16)
+    g = torch.Generator(device=device).manual_seed(seed)
+    t_dist = torch.distributions.StudentT(torch.tensor(3.0, device=device))
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dim() == 1:
+                p.fill_(1.0)
+                continue
+            w = torch.randn(p.shape, generator=g, device=device, dtype=torch.float32) * 0.02
+            mask = torch.rand(p.shape, generator=g, device=device) < 0.001
+            w[mask] = (0.02 * t_dist.sample((int(mask.sum()),))).float()
+            p.copy_(w.to(torch.bfloat16))
+            del w, mask
+        # buffers were created uninitialized; the rotary frequencies stay fp32
+        head = LLAMA3_8B["hidden_size"] // LLAMA3_8B["num_attention_heads"]
+        model.model.rotary_emb.inv_freq = 1.0 / (LLAMA3_8B["rope_theta"] ** (
+            torch.arange(0, head, 2, device=device, dtype=torch.float32) / head))
+    return model.eval()
+
+
+def time_generate(model, ids, new_tokens):
+    """(decode-phase seconds for new_tokens - 1 tokens, generated ids): the
+    time of generating new_tokens minus the time of generating one."""
+    def run(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = model.generate(ids, max_new_tokens=n, min_new_tokens=n, do_sample=False, use_cache=True,
+                             pad_token_id=0)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, out
+    run(2)   # warm
+    first, _ = run(1)
+    full, out = run(new_tokens)
+    return full - first, out
+
+
+def model_benchmark(args):
+    """tok/s of greedy generation on the Llama-3-8B shape, NeuralZip runtime
+    against the same model uncompressed in bf16."""
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    device = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    model = random_llama(device)
+    log(f"model built in {time.perf_counter() - t0:.1f}s")
+    ids = torch.randint(0, LLAMA3_8B["vocab_size"], (args.batch, args.prompt),
+                        generator=torch.Generator().manual_seed(3)).to(device)
+    with torch.no_grad():
+        ref_logits = model(ids[:, :64]).logits.float().cpu()
+    base_s, base_out = time_generate(model, ids, args.new_tokens)
+    log(f"bf16: {base_s * 1e3:.1f} ms for {args.new_tokens - 1} decode steps")
+    t0 = time.perf_counter()
+    model = model.cpu()
+    torch.cuda.empty_cache()
+    setup = NeuralZipSetup(cluster_js_threshold=0.05).build(model)
+    log(f"setup: {len(setup.codebooks)} codebooks in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    exported = export_model_for_gpu(model, setup)
+    runtime = NeuralZipRuntime.attach(model, exported, device=device)
+    log(f"export + attach: {len(exported.groups)} fragments, {len(exported.block_order)} blocks "
+        f"in {time.perf_counter() - t0:.1f}s")
+    with torch.no_grad():
+        logits = model(ids[:, :64]).logits.float().cpu()
+    # one decode of every compressed block, back to back on one stream
+    stream = torch.cuda.current_stream(device)
+    for name in exported.block_order:
+        runtime._launch(name, stream)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    passes = 5
+    a.record(stream)
+    for _ in range(passes):
+        for name in exported.block_order:
+            runtime._launch(name, stream)
+    b.record(stream)
+    torch.cuda.synchronize(device)
+    pass_ms = a.elapsed_time(b) / passes
+    decoded_bytes = sum(g.encoded.raw_bytes for g in exported.groups)
+    log(f"full decode pass: {pass_ms:.3f} ms, {decoded_bytes / pass_ms / 1e6:.0f} GB/s decoded")
+    nz_s, nz_out = time_generate(model, ids, args.new_tokens)
+    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {args.new_tokens - 1} decode steps")
+    steps = args.new_tokens - 1
+    tok_s = args.batch * steps / nz_s
+    base_tok_s = args.batch * steps / base_s
+    line = {
+        "metric": f"tok/s 8B-shape bs={args.batch} vs uncompressed bf16",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 1,
+        "ms_per_step": round(nz_s / steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"Llama-3-8B shape (hidden 4096, intermediate 14336, 32 layers, 32 heads, 8 KV heads, "
+                               f"vocab 128256, untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3), greedy "
+                               f"generation, batch {args.batch}, {args.prompt} prompt + {args.new_tokens} new tokens, "
+                               f"decode phase timed",
+                   "compressed_blocks": len(exported.block_order),
+                   "full_decode_pass_ms": round(pass_ms, 3),
+                   "full_decode_pass_gbps": round(decoded_bytes / pass_ms / 1e6, 1),
+                   "decoded_bytes_per_pass": int(decoded_bytes),
+                   "fragments": len(exported.groups),
+                   "prefetch": runtime.prefetch},
+        "bf16_tok_s": round(base_tok_s, 2),
+        "ratio_vs_bf16": round(base_tok_s / tok_s, 3),
+        "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
+        "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if line["logits_bitwise_equal"] and line["tokens_identical"] else 1
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -125,9 +253,19 @@ def main():
                         help="decode workgroups per launch (default: what the device runs at once)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain 1 GiB device copy (calibrates HBM byte counters)")
+    parser.add_argument("--model", choices=["llama3-8b"], default=None,
+                        help="model-level tok/s against uncompressed bf16 instead of the kernel benchmark")
+    parser.add_argument("--batch", type=int, default=1)
+    parser.add_argument("--prompt", type=int, default=512)
+    parser.add_argument("--new-tokens", type=int, default=256)
     args = parser.parse_args()
     if args.copy_calibration:
         return copy_calibration()
+    if args.model:
+        if args.gpus != 1:
+            print("bench.py measures one GPU; run with --gpus 1.", file=sys.stderr)
+            return 2
+        return model_benchmark(args)
     if args.gpus != 1:
         print("bench.py measures one GPU: decode needs no collective and this build runs on one device; "
               "run with --gpus 1.", file=sys.stderr)

@@ -13,7 +13,7 @@ stream (which includes the last reads of that slot, by block N-1).
 """
 from collections import defaultdict
 from dataclasses import dataclass, field
-from functools import partial
+from functools import cached_property, partial
 
 import numpy as np
 import torch
@@ -176,11 +176,11 @@ class NeuralZipModelExport:
     tensors: tuple = field(default=(), repr=False)   # (layout, codebook ids, offset, dtype, block name)
     codebooks: dict = field(default_factory=dict, repr=False)
 
-    @property
+    @cached_property
     def block_order(self):
         return tuple(dict.fromkeys(group.block_name for group in self.groups))
 
-    @property
+    @cached_property
     def bindings(self):
         return tuple(dict.fromkeys(binding for group in self.groups for binding in group.bindings))
 
@@ -346,6 +346,8 @@ class NeuralZipRuntime:
         self._decoder = gpu_decoder.default_decoder()
         self._hook_handles = []
         order = exported.block_order
+        # block -> the block whose decode its hook prefetches (the first after the last)
+        self._following = {name: order[(i + 1) % len(order)] for i, name in enumerate(order)}
         n_slots = 1 if not self.prefetch or len(order) < 2 else (2 if len(order) % 2 == 0 else 3)
         self.block_slot = {name: (i % 2 if n_slots > 1 else 0) for i, name in enumerate(order)}
         if n_slots == 3:
@@ -444,8 +446,7 @@ class NeuralZipRuntime:
             self._launch(block_name, current)
         if self.side_stream is None:
             return
-        order = self.export.block_order
-        following = order[(order.index(block_name) + 1) % len(order)]
+        following = self._following[block_name]
         if following == block_name:
             return
         # everything queued so far (the last readers of `following`'s slot
