@@ -121,3 +121,28 @@ def test_work_partitions_give_identical_output(slots):
              1: _native.Codebook(singleton_header(raw[: 20000], torch.bfloat16, prior=3))}
     ids = [(0, 1, -1)[j % 3] for j in range(-(-1000000 // 65536))]
     check_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, slots=slots)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_tiny_fragments_at_every_vector_phase(dtype):
+    """Fragments of 1..129 elements at output offsets of every phase within a
+    16-byte vector: single-window tiles, partial first and last vectors,
+    a pair parse that stops before the last element."""
+    spec = DTYPES[dtype]
+    V = 16 // spec.element_size
+    rng = np.random.default_rng(21)
+    vocab = bytes((127, 127, 125, 126))
+    lengths = segment_lengths(16) if dtype is not torch.float16 else None
+    book = (_native.Codebook(b"NZM1" + lengths, vocab) if lengths is not None
+            else _native.Codebook(singleton_header(
+                (torch.randn(4096) * 0.05).to(dtype).view(torch.uint8).numpy().reshape(-1), dtype)))
+    tensors, offset = [], 3
+    for k, n in enumerate([1, 2, 3, 7, 8, 9, 15, 16, 17, 63, 64, 65, 127, 128, 129]):
+        if lengths is not None:
+            symbols = rng.choice([127, 125, 126, 3, 200], n).astype(np.uint8)
+            raw = segment_tensor(dtype, symbols)
+        else:
+            raw = (torch.randn(n) * 0.05).to(dtype).view(torch.uint8).numpy().reshape(-1).copy()
+        tensors.append((raw, dtype, 1 << 20, [0], offset))
+        offset += n + (k % V) + 1
+    check_case(tensors, {0: book}, dtype)

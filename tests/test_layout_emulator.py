@@ -190,3 +190,25 @@ def test_plan_shares_workgroups_by_elements():
     # fewer slots than runs: one workgroup per run
     segments = _native.plan_work(descs, tiles, 1)
     assert segments[["tile0", "tile1"]].tolist() == [(0, 3), (3, 4), (4, 6)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_tiny_fragments_at_every_vector_phase(dtype):
+    spec = DTYPES[dtype]
+    V = 16 // spec.element_size
+    rng = np.random.default_rng(21)
+    vocab = bytes((127, 127, 125, 126))
+    if dtype is torch.float16:
+        book = _native.Codebook(singleton_header(
+            (torch.randn(4096) * 0.05).to(dtype).view(torch.uint8).numpy().reshape(-1), dtype))
+    else:
+        book = _native.Codebook(b"NZM1" + segment_lengths(16), vocab)
+    tensors, offset = [], 3
+    for k, n in enumerate([1, 2, 3, 7, 8, 9, 15, 16, 17, 63, 64, 65, 127, 128, 129]):
+        if dtype is torch.float16:
+            raw = (torch.randn(n) * 0.05).to(dtype).view(torch.uint8).numpy().reshape(-1).copy()
+        else:
+            raw = segment_tensor(dtype, rng.choice([127, 125, 126, 3, 200], n).astype(np.uint8))
+        tensors.append((raw, dtype, 1 << 20, [0], offset))
+        offset += n + (k % V) + 1
+    emulate_case(tensors, {0: book}, dtype)
