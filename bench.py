@@ -118,33 +118,50 @@ def copy_bandwidth(device, nbytes=1 << 30, repeats=10):
 LLAMA3_8B = dict(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
                  num_key_value_heads=8, vocab_size=128256, max_position_embeddings=8192, rope_theta=500000.0,
                  tie_word_embeddings=False)
+QWEN2_05B = dict(hidden_size=896, intermediate_size=4864, num_hidden_layers=24, num_attention_heads=14,
+                 num_key_value_heads=2, vocab_size=151936, max_position_embeddings=32768, rope_theta=1000000.0,
+                 tie_word_embeddings=True)
+MODELS = {
+    # name: (config class name, shape, outliers, default prompt, default new tokens, description)
+    "llama3-8b": ("LlamaConfig", LLAMA3_8B, True, 512, 256,
+                  "Llama-3-8B shape (hidden 4096, intermediate 14336, 32 layers, 32 heads, 8 KV heads, vocab 128256, "
+                  "untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
+    "qwen2-0.5b": ("Qwen2Config", QWEN2_05B, False, 128, 128,
+                   "Qwen2-0.5B shape (hidden 896, intermediate 4864, 24 layers, 14 heads, 2 KV heads, head_dim 64, "
+                   "vocab 151936, tied embeddings), random bf16 weights N(0, 0.02^2)"),
+}
 
 
-def random_llama(device, seed=1):
-    """Llama-3-8B-shaped model with bf16 random weights: linears and
-    embeddings N(0, 0.02^2) with 0.1 % of entries replaced by
-    0.02 * Student-t(3), norms 1 (config 4 of the survey)."""
-    from transformers import LlamaConfig, LlamaForCausalLM
-    config = LlamaConfig(**LLAMA3_8B, torch_dtype=torch.bfloat16)
+def random_model(kind, device, seed=1):
+    """A causal LM of one of MODELS' shapes with bf16 random weights:
+    matrices N(0, 0.02^2) (0.1 % replaced by 0.02 * Student-t(3) where the
+    shape asks for outliers), norms 1, biases 0."""
+    import transformers
+    config_name, shape, outliers, _, _, _ = MODELS[kind]
+    config = getattr(transformers, config_name)(**shape, torch_dtype=torch.bfloat16)
     with torch.device("meta"):
-        model = LlamaForCausalLM(config)
+        model = transformers.AutoModelForCausalLM.from_config(config)
     model = model.to_empty(device=device).to(torch.bfloat16)
     g = torch.Generator(device=device).manual_seed(seed)
     t_dist = torch.distributions.StudentT(torch.tensor(3.0, device=device))
     with torch.no_grad():
         for name, p in model.named_parameters():
             if p.dim() == 1:
-                p.fill_(1.0)
+                p.fill_(1.0 if "norm" in name else 0.0)
                 continue
             w = torch.randn(p.shape, generator=g, device=device, dtype=torch.float32) * 0.02
-            mask = torch.rand(p.shape, generator=g, device=device) < 0.001
-            w[mask] = (0.02 * t_dist.sample((int(mask.sum()),))).float()
+            if outliers:
+                mask = torch.rand(p.shape, generator=g, device=device) < 0.001
+                w[mask] = (0.02 * t_dist.sample((int(mask.sum()),))).float()
+                del mask
             p.copy_(w.to(torch.bfloat16))
-            del w, mask
+            del w
         # buffers were created uninitialized; the rotary frequencies stay fp32
-        head = LLAMA3_8B["hidden_size"] // LLAMA3_8B["num_attention_heads"]
-        model.model.rotary_emb.inv_freq = 1.0 / (LLAMA3_8B["rope_theta"] ** (
+        head = shape["hidden_size"] // shape["num_attention_heads"]
+        model.model.rotary_emb.inv_freq = 1.0 / (shape["rope_theta"] ** (
             torch.arange(0, head, 2, device=device, dtype=torch.float32) / head))
+    if shape["tie_word_embeddings"]:
+        model.tie_weights()
     return model.eval()
 
 
@@ -165,20 +182,24 @@ def time_generate(model, ids, new_tokens):
 
 
 def model_benchmark(args):
-    """tok/s of greedy generation on the Llama-3-8B shape, NeuralZip runtime
-    against the same model uncompressed in bf16."""
+    """tok/s of greedy generation on a model shape of MODELS, NeuralZip
+    runtime against the same model uncompressed in bf16, with the prompt's
+    logits and every generated token compared bit for bit."""
     from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
     from neuralzip_amd.setup import NeuralZipSetup
     device = torch.device("cuda:0")
+    _, shape, _, default_prompt, default_new, description = MODELS[args.model]
+    prompt = args.prompt or default_prompt
+    new_tokens = args.new_tokens or default_new
     t0 = time.perf_counter()
-    model = random_llama(device)
+    model = random_model(args.model, device)
     log(f"model built in {time.perf_counter() - t0:.1f}s")
-    ids = torch.randint(0, LLAMA3_8B["vocab_size"], (args.batch, args.prompt),
+    ids = torch.randint(0, shape["vocab_size"], (args.batch, prompt),
                         generator=torch.Generator().manual_seed(3)).to(device)
     with torch.no_grad():
         ref_logits = model(ids[:, :64]).logits.float().cpu()
-    base_s, base_out = time_generate(model, ids, args.new_tokens)
-    log(f"bf16: {base_s * 1e3:.1f} ms for {args.new_tokens - 1} decode steps")
+    base_s, base_out = time_generate(model, ids, new_tokens)
+    log(f"bf16: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps")
     t0 = time.perf_counter()
     model = model.cpu()
     torch.cuda.empty_cache()
@@ -206,13 +227,13 @@ def model_benchmark(args):
     pass_ms = a.elapsed_time(b) / passes
     decoded_bytes = sum(g.encoded.raw_bytes for g in exported.groups)
     log(f"full decode pass: {pass_ms:.3f} ms, {decoded_bytes / pass_ms / 1e6:.0f} GB/s decoded")
-    nz_s, nz_out = time_generate(model, ids, args.new_tokens)
-    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {args.new_tokens - 1} decode steps")
-    steps = args.new_tokens - 1
+    nz_s, nz_out = time_generate(model, ids, new_tokens)
+    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {new_tokens - 1} decode steps")
+    steps = new_tokens - 1
     tok_s = args.batch * steps / nz_s
     base_tok_s = args.batch * steps / base_s
     line = {
-        "metric": f"tok/s 8B-shape bs={args.batch} vs uncompressed bf16",
+        "metric": f"tok/s {args.model} shape bs={args.batch} vs uncompressed bf16",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -224,10 +245,8 @@ def model_benchmark(args):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"Llama-3-8B shape (hidden 4096, intermediate 14336, 32 layers, 32 heads, 8 KV heads, "
-                               f"vocab 128256, untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3), greedy "
-                               f"generation, batch {args.batch}, {args.prompt} prompt + {args.new_tokens} new tokens, "
-                               f"decode phase timed",
+        "config": {"workload": f"{description}, greedy generation, batch {args.batch}, {prompt} prompt + "
+                               f"{new_tokens} new tokens, decode phase timed",
                    "compressed_blocks": len(exported.block_order),
                    "full_decode_pass_ms": round(pass_ms, 3),
                    "full_decode_pass_gbps": round(decoded_bytes / pass_ms / 1e6, 1),
@@ -253,11 +272,11 @@ def main():
                         help="decode workgroups per launch (default: what the device runs at once)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain 1 GiB device copy (calibrates HBM byte counters)")
-    parser.add_argument("--model", choices=["llama3-8b"], default=None,
+    parser.add_argument("--model", choices=sorted(MODELS), default=None,
                         help="model-level tok/s against uncompressed bf16 instead of the kernel benchmark")
     parser.add_argument("--batch", type=int, default=1)
-    parser.add_argument("--prompt", type=int, default=512)
-    parser.add_argument("--new-tokens", type=int, default=256)
+    parser.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the model's)")
+    parser.add_argument("--new-tokens", type=int, default=None, help="generated tokens (default: the model's)")
     args = parser.parse_args()
     if args.copy_calibration:
         return copy_calibration()
