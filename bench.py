@@ -266,7 +266,8 @@ def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=10)
+    # the device's clocks settle over the first ~30 launches of this kernel
+    parser.add_argument("--warmup", type=int, default=40)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--slots", type=int, default=None,
                         help="decode workgroups per launch (default: what the device runs at once)")
