@@ -123,7 +123,8 @@ int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base,
  * LUT and kind are adjacent: one segment (nz_work record: a contiguous tile
  * range of one LUT and kind) per workgroup. Maximal runs of one LUT and kind
  * share out `slots` workgroups (the number the device runs at once, from
- * nz_decode_slots; at least one per run) in proportion to their elements and
+ * nz_decode_slots; at least one per run, at most one per 16 tiles) in
+ * proportion to their elements and
  * are cut into that many segments of about equal elements. With
  * segments == NULL only *n_segments is set.
  * Replaces: the block->group / block->local id tensors (decoder.py:168-179). */

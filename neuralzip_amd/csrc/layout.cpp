@@ -207,6 +207,8 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
     d->reserved = 0;
 }
 
+constexpr uint64_t kMinTilesPerGroup = 16;
+
 std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
     std::vector<nz_work> runs;   // maximal runs of one LUT and kind
     if (!n_tiles) return runs;
@@ -230,7 +232,10 @@ std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, 
         }
     }
     const size_t n_seg = runs.size();
-    const uint64_t groups = std::max<uint64_t>(slots, n_seg);
+    // Small launches get fewer workgroups: each one stages a whole LUT image,
+    // so it should have at least a tile per wavefront to decode.
+    const uint64_t enough = (n_tiles + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
+    const uint64_t groups = std::max<uint64_t>(std::min<uint64_t>(slots, enough), n_seg);
     std::vector<uint64_t> share(n_seg, 1);
     double total = 0;
     for (double c : cost) total += c;

@@ -53,8 +53,9 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 // Launch plan over `n_tiles` tiles (callers order them so that tiles of one
 // LUT and kind are adjacent): one segment per workgroup. Maximal runs of one
 // LUT and kind share out `slots` workgroups (the number the device runs at
-// once; at least one per run) in proportion to their elements, and each run
-// is cut into that many contiguous segments of about equal elements.
+// once; at least one per run, and no more than one per 16 tiles) in
+// proportion to their elements, and each run is cut into that many
+// contiguous segments of about equal elements.
 std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots);
 
 // CPU emulation of the decode kernel over a packed buffer; writes words

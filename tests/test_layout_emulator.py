@@ -176,20 +176,23 @@ def test_plan_shares_workgroups_by_elements():
     descs = np.zeros(3, dtype=_native.FRAG_DESC)
     descs["kind"] = [_native.KIND_SHORT, _native.KIND_SHORT, _native.KIND_RAW]
     descs["lut"] = [0, 4096, 0]
-    tiles = np.zeros(6, dtype=_native.TILE)
-    tiles["frag"] = [0, 0, 0, 1, 2, 2]
-    tiles["n_out"] = [1000, 1000, 1000, 1000, 2000, 2000]   # raw tiles count half
-    # runs of 3000, 1000 and 2000 (raw at half) elements; 5 slots: one each,
-    # then 2 more split 1.0 : 0.33 : 0.67 -> the first and the raw run
+    frags = [0] * 96 + [1] * 32 + [2] * 64
+    tiles = np.zeros(len(frags), dtype=_native.TILE)
+    tiles["frag"] = frags
+    tiles["n_out"] = [1000] * 128 + [2000] * 64   # raw tiles count half
+    # runs of 96000, 32000 and 64000 (raw at half) elements; 5 slots: one
+    # each, then 2 more split 1.0 : 0.33 : 0.67 -> the first and the raw run
     segments = _native.plan_work(descs, tiles, 5)
-    assert segments[["tile0", "tile1"]].tolist() == [(0, 2), (2, 3), (3, 4), (4, 5), (5, 6)]
+    assert segments[["tile0", "tile1"]].tolist() == [(0, 48), (48, 96), (96, 128), (128, 160), (160, 192)]
     assert segments["kind"].tolist() == [_native.KIND_SHORT] * 3 + [_native.KIND_RAW] * 2
-    # a run is never cut into more segments than it has tiles
-    segments = _native.plan_work(descs, tiles, 100)
-    assert segments[["tile0", "tile1"]].tolist() == [(0, 1), (1, 2), (2, 3), (3, 4), (4, 5), (5, 6)]
+    # at most one workgroup per 16 tiles: 192 tiles -> 12 groups however many slots
+    assert len(_native.plan_work(descs, tiles, 100)) == 12
     # fewer slots than runs: one workgroup per run
     segments = _native.plan_work(descs, tiles, 1)
-    assert segments[["tile0", "tile1"]].tolist() == [(0, 3), (3, 4), (4, 6)]
+    assert segments[["tile0", "tile1"]].tolist() == [(0, 96), (96, 128), (128, 192)]
+    # a run is never cut into more segments than it has tiles
+    few = tiles[[0, 1, 96, 128, 129]]
+    assert len(_native.plan_work(descs, few, 100)) == 3
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
