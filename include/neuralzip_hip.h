@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 1
+#define NZ_ABI_VERSION 2
 
 enum nz_status {
     NZ_OK = 0,

@@ -57,10 +57,8 @@ class _Totals(ctypes.Structure):
 
 
 _lib = None
-EXPORTS = ("nz_last_error", "nz_abi_version", "nz_codebook_create", "nz_codebook_destroy", "nz_codebook_export",
-           "nz_codebook_lut", "nz_layout_encode", "nz_layout_destroy", "nz_layout_totals_get",
-           "nz_layout_fragment_info", "nz_layout_pack", "nz_plan_work", "nz_decode_slots", "nz_decode_launch",
-           "nz_emulate_decode")
+# The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
+ABI_VERSION = 2
 
 
 def lib():
@@ -69,6 +67,9 @@ def lib():
         if not LIBRARY.exists():
             raise ImportError(f"{LIBRARY} is not built; run `python -m neuralzip_amd.build` first.")
         L = ctypes.CDLL(str(LIBRARY))
+        if L.nz_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIBRARY} has C ABI version {L.nz_abi_version()}, these bindings need "
+                              f"{ABI_VERSION}; rebuild it with `python -m neuralzip_amd.build`.")
         vp, u32, u64, sz = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_size_t
         L.nz_last_error.restype = ctypes.c_char_p
         L.nz_codebook_create.argtypes = [vp, sz, vp, sz, ctypes.POINTER(vp)]

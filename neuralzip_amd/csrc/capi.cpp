@@ -45,7 +45,7 @@ extern "C" {
 
 const char* nz_last_error(void) { return g_error.c_str(); }
 
-int nz_abi_version(void) { return 1; }
+int nz_abi_version(void) { return NZ_ABI_VERSION; }
 
 int nz_codebook_create(const uint8_t* header, size_t header_size, const uint8_t* vocab, size_t vocab_size,
                        nz_codebook** out) {

@@ -14,7 +14,6 @@ import torch
 from neuralzip_amd import _native
 from neuralzip_amd._native import FRAG_DESC, KIND_LONG, KIND_RAW, TILE
 
-THREADS_PER_BLOCK = 256
 WINDOW_BITS = 64
 # Workgroups per launch: None asks the device how many decode workgroups it
 # runs at once (two 16-wavefront workgroups per CU on MI355X, 512 in all), so
@@ -78,7 +77,6 @@ class DeviceStore:
         self.tiles = np.concatenate(tiles) if tiles else np.zeros(0, TILE)
         self.tile_starts = np.asarray(tile_starts, dtype=np.int64)
         self.frags = torch.from_numpy(self.descs.view(np.uint8).copy()).to(self.device)
-        self.frag_base = {}
 
     def fragment_tiles(self, index):
         return self.tiles[self.tile_starts[index]:self.tile_starts[index + 1]]

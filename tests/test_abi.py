@@ -1,0 +1,61 @@
+"""The C ABI without a GPU: the library loads, exports every function the
+public header declares, reports the header's ABI version, and lays out the
+device descriptors as the header and the bindings say."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from neuralzip_amd import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "neuralzip_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(nz_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_documented_entry_points():
+    names = declared_functions()
+    for expected in ("nz_last_error", "nz_abi_version", "nz_codebook_create", "nz_layout_encode", "nz_layout_pack",
+                     "nz_plan_work", "nz_decode_slots", "nz_decode_launch", "nz_storage_compress",
+                     "nz_storage_decompress"):
+        assert expected in names
+
+
+def test_library_exports_every_declared_function():
+    lib = ctypes.CDLL(str(_native.LIBRARY))
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing, missing
+
+
+def test_abi_version_matches_header_and_bindings():
+    version = int(re.search(r"#define NZ_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert ctypes.CDLL(str(_native.LIBRARY)).nz_abi_version() == version == _native.ABI_VERSION
+    _native.lib()   # loads with the version check
+
+
+def test_descriptor_layouts_match_the_format_header(tmp_path):
+    probe = tmp_path / "sizes.cpp"
+    probe.write_text(
+        '#include <cstddef>\n#include <cstdio>\n#include "nz_format.h"\n'
+        "int main(void) {\n"
+        '  printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(struct nz_frag_desc), sizeof(struct nz_tile),\n'
+        "         sizeof(struct nz_work), offsetof(struct nz_frag_desc, bit_length), offsetof(struct nz_frag_desc, numel),\n"
+        "         offsetof(struct nz_tile, counts), offsetof(struct nz_work, kind));\n"
+        "  return 0;\n}\n")
+    exe = tmp_path / "sizes"
+    try:
+        built = subprocess.run(["g++", "-std=c++17", "-I", str(ROOT / "neuralzip_amd" / "csrc"), str(probe), "-o",
+                                str(exe)], capture_output=True, text=True)
+    except FileNotFoundError:
+        pytest.skip("no C++ compiler for the layout probe")
+    assert built.returncode == 0, built.stderr
+    sizes = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert sizes == [_native.FRAG_DESC.itemsize, _native.TILE.itemsize, _native.WORK.itemsize,
+                     _native.FRAG_DESC.fields["bit_length"][1], _native.FRAG_DESC.fields["numel"][1],
+                     _native.TILE.fields["shape"][1], _native.WORK.fields["kind"][1]]
