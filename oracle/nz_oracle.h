@@ -3,8 +3,9 @@
  *
  * The oracle is a plain-C CPU restatement of the reference's codec for the
  * exponent-lane decompression path. Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load it, and only as the checker (or as the
- * timed CPU baseline); the product library never links or calls it.
+ * bench.py's cpu_baseline leg may load it, and only to check the product's
+ * results (or as the timed CPU baseline); the product library never links or
+ * calls it.
  *
  * Every function cites the reference file:line it restates. The Huff0 parts
  * restate RFC 8878 sections 4.1 (FSE) and 4.2 (Huffman), because the reference
