@@ -95,6 +95,8 @@ class PreparedBatch:
     output: torch.Tensor = field(repr=False)
     outputs: tuple = field(repr=False, default=())
     algorithmic_bytes: int = 0
+    # nz_decode_launch arguments but the stream, fixed at prepare time
+    launch_args: tuple = field(repr=False, default=())
 
 
 def layout_key(desc, dtype):
@@ -134,8 +136,10 @@ class HIPDecoder:
         segments = _native.plan_work(store.descs, tiles, slots)
         tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
         segments_t = torch.from_numpy(segments.view(np.uint8).copy()).to(device)
+        args = (store.buffer.data_ptr(), store.frags.data_ptr(), tiles_t.data_ptr(), segments_t.data_ptr(),
+                len(segments), key[0], int(key[1]), int(key[2]), output.data_ptr())
         return PreparedBatch((tiles_t, segments_t), device, key, (len(segments),), len(segments), store, output,
-                             tuple(outputs), algorithmic_bytes(store.descs[fragment_indices], dtype))
+                             tuple(outputs), algorithmic_bytes(store.descs[fragment_indices], dtype), args)
 
     def slots(self, device, key):
         """Decode workgroups `device` runs at once for layout `key` (cached)."""
@@ -147,13 +151,11 @@ class HIPDecoder:
         return cache[(device, key)]
 
     def decode_batch(self, prepared, stream=None):
+        """Launches the batch on `stream` (default: the current stream); the
+        batch holds its device arrays, so the saved pointers stay valid."""
         if stream is None:
             stream = torch.cuda.current_stream(prepared.device)
-        tiles_t, segments_t = prepared.descriptor_tensors
-        element_size, bit_reorder, long_codes = prepared.layout
-        _native.decode_launch(prepared.store.buffer.data_ptr(), prepared.store.frags.data_ptr(),
-                              tiles_t.data_ptr(), segments_t.data_ptr(), prepared.n_segments, element_size,
-                              bit_reorder, long_codes, prepared.output.data_ptr(), stream.cuda_stream)
+        _native.decode_launch(*prepared.launch_args, stream.cuda_stream)
         return prepared.outputs
 
 

@@ -386,6 +386,8 @@ class NeuralZipRuntime:
         for group in exported.groups:
             self._groups_by_block[group.block_name].append(group)
         self.side_stream = torch.cuda.Stream(self.device) if self.prefetch else None
+        with torch.cuda.device(self.device):
+            self._events = {name: (torch.cuda.Event(), torch.cuda.Event()) for name in order} if self.prefetch else {}
         self._pending = None   # (block name, event) decoded ahead on the side stream
         torch.cuda.synchronize(self.device)
 
@@ -450,12 +452,12 @@ class NeuralZipRuntime:
         if following == block_name:
             return
         # everything queued so far (the last readers of `following`'s slot
-        # included) completes before the side stream overwrites that slot
-        ready = torch.cuda.Event()
+        # included) completes before the side stream overwrites that slot;
+        # an event's later records do not change waits already queued on it
+        ready, done = self._events[following]
         ready.record(current)
         self.side_stream.wait_event(ready)
         self._launch(following, self.side_stream)
-        done = torch.cuda.Event()
         done.record(self.side_stream)
         self._pending = (following, done)
 
