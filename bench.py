@@ -118,6 +118,9 @@ def copy_bandwidth(device, nbytes=1 << 30, repeats=10):
 LLAMA3_8B = dict(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
                  num_key_value_heads=8, vocab_size=128256, max_position_embeddings=8192, rope_theta=500000.0,
                  tie_word_embeddings=False)
+LLAMA3_70B = dict(hidden_size=8192, intermediate_size=28672, num_hidden_layers=80, num_attention_heads=64,
+                  num_key_value_heads=8, vocab_size=128256, max_position_embeddings=8192, rope_theta=500000.0,
+                  tie_word_embeddings=False)
 QWEN2_05B = dict(hidden_size=896, intermediate_size=4864, num_hidden_layers=24, num_attention_heads=14,
                  num_key_value_heads=2, vocab_size=151936, max_position_embeddings=32768, rope_theta=1000000.0,
                  tie_word_embeddings=True)
@@ -126,6 +129,9 @@ MODELS = {
     "llama3-8b": ("LlamaConfig", LLAMA3_8B, True, 512, 256,
                   "Llama-3-8B shape (hidden 4096, intermediate 14336, 32 layers, 32 heads, 8 KV heads, vocab 128256, "
                   "untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
+    "llama3-70b": ("LlamaConfig", LLAMA3_70B, True, 256, 128,
+                   "Llama-3-70B shape (hidden 8192, intermediate 28672, 80 layers, 64 heads, 8 KV heads, vocab "
+                   "128256, untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
     "qwen2-0.5b": ("Qwen2Config", QWEN2_05B, False, 128, 128,
                    "Qwen2-0.5B shape (hidden 896, intermediate 4864, 24 layers, 14 heads, 2 KV heads, head_dim 64, "
                    "vocab 151936, tied embeddings), random bf16 weights N(0, 0.02^2)"),
@@ -141,7 +147,7 @@ def random_model(kind, device, seed=1):
     config = getattr(transformers, config_name)(**shape, torch_dtype=torch.bfloat16)
     with torch.device("meta"):
         model = transformers.AutoModelForCausalLM.from_config(config)
-    model = model.to_empty(device=device).to(torch.bfloat16)
+    model = model.to(torch.bfloat16).to_empty(device=device)   # bf16 from the start: 70B fits
     g = torch.Generator(device=device).manual_seed(seed)
     t_dist = torch.distributions.StudentT(torch.tensor(3.0, device=device))
     with torch.no_grad():
@@ -198,12 +204,20 @@ def model_benchmark(args):
                         generator=torch.Generator().manual_seed(3)).to(device)
     with torch.no_grad():
         ref_logits = model(ids[:, :64]).logits.float().cpu()
+    torch.cuda.reset_peak_memory_stats(device)
     base_s, base_out = time_generate(model, ids, new_tokens)
-    log(f"bf16: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps")
+    base_peak = torch.cuda.max_memory_allocated(device)
+    log(f"bf16: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {base_peak / 2**30:.1f} GiB")
     t0 = time.perf_counter()
-    model = model.cpu()
-    torch.cuda.empty_cache()
-    setup = NeuralZipSetup(cluster_js_threshold=0.05).build(model)
+    # setup and export read each weight back from the device one at a time
+    marks = {}
+
+    def progress(done, total, name):
+        decile = 10 * done // total
+        if decile not in marks:
+            marks[decile] = True
+            log(f"setup: {done}/{total} tensors clustered ({time.perf_counter() - t0:.0f}s)")
+    setup = NeuralZipSetup(cluster_js_threshold=0.05).build(model, progress=progress)
     log(f"setup: {len(setup.codebooks)} codebooks in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     exported = export_model_for_gpu(model, setup)
@@ -227,8 +241,11 @@ def model_benchmark(args):
     pass_ms = a.elapsed_time(b) / passes
     decoded_bytes = sum(g.encoded.raw_bytes for g in exported.groups)
     log(f"full decode pass: {pass_ms:.3f} ms, {decoded_bytes / pass_ms / 1e6:.0f} GB/s decoded")
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats(device)
     nz_s, nz_out = time_generate(model, ids, new_tokens)
-    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {new_tokens - 1} decode steps")
+    nz_peak = torch.cuda.max_memory_allocated(device)
+    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {nz_peak / 2**30:.1f} GiB")
     steps = new_tokens - 1
     tok_s = args.batch * steps / nz_s
     base_tok_s = args.batch * steps / base_s
@@ -251,6 +268,9 @@ def model_benchmark(args):
                    "full_decode_pass_ms": round(pass_ms, 3),
                    "full_decode_pass_gbps": round(decoded_bytes / pass_ms / 1e6, 1),
                    "decoded_bytes_per_pass": int(decoded_bytes),
+                   "compressed_store_bytes": int(runtime.store.nbytes),
+                   "peak_allocated_bf16_gib": round(base_peak / 2**30, 2),
+                   "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
                    "prefetch": runtime.prefetch},
         "bf16_tok_s": round(base_tok_s, 2),

@@ -76,8 +76,12 @@ class NeuralZipSetup:
     def setup_seconds(self):
         return self.setup_report.setup_seconds
 
-    def build(self, model):
-        (groups, assignments, parents), clustering = time_call(self._cluster_chunks, _model_tensors(model))
+    def build(self, model, *, progress=None):
+        """Cluster the chunks of `model` (a module or a tensor mapping) and
+        build the cluster codebooks. `progress(done, total, name)`, when
+        given, is called after each tensor's chunks are clustered."""
+        (groups, assignments, parents), clustering = time_call(self._cluster_chunks, _model_tensors(model),
+                                                               progress)
         (books, chunks, tensors, report), codebook_seconds = time_call(self._build_codebooks, groups,
                                                                        assignments, parents)
         self.codebooks = tuple(books)
@@ -105,10 +109,11 @@ class NeuralZipSetup:
         return value
 
     # -------------------------------------------------------- clustering
-    def _cluster_chunks(self, named_tensors):
+    def _cluster_chunks(self, named_tensors, progress=None):
         """Greedy JS clustering of chunk exponent histograms (setup.py:91-141)."""
         groups, assignments, parents = [], {}, {}
-        for name, tensor in _floating_tensors(named_tensors):
+        tensors = list(_floating_tensors(named_tensors))
+        for done, (name, tensor) in enumerate(tensors, 1):
             spec = DTYPES[tensor.dtype]
             raw = _tensor_raw_bytes(tensor)
             stream_id = spec.selected_stream
@@ -143,6 +148,8 @@ class NeuralZipSetup:
                     group["sampled"] += len(sample)
                 ids.append(nearest)
             assignments[(*key, tensor.numel())] = tuple(ids)
+            if progress is not None:
+                progress(done, len(tensors), name)
         return groups, assignments, parents
 
     # -------------------------------------------------------- codebooks
