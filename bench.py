@@ -128,26 +128,29 @@ MODELS = {
     # name: (config class name, shape, outliers, default prompt, default new tokens, description)
     "llama3-8b": ("LlamaConfig", LLAMA3_8B, True, 512, 256,
                   "Llama-3-8B shape (hidden 4096, intermediate 14336, 32 layers, 32 heads, 8 KV heads, vocab 128256, "
-                  "untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
+                  "untied), random {dtype} weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
     "llama3-70b": ("LlamaConfig", LLAMA3_70B, True, 256, 128,
                    "Llama-3-70B shape (hidden 8192, intermediate 28672, 80 layers, 64 heads, 8 KV heads, vocab "
-                   "128256, untied), random bf16 weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
+                   "128256, untied), random {dtype} weights N(0, 0.02^2) + 0.1% 0.02*t(3)"),
     "qwen2-0.5b": ("Qwen2Config", QWEN2_05B, False, 128, 128,
                    "Qwen2-0.5B shape (hidden 896, intermediate 4864, 24 layers, 14 heads, 2 KV heads, head_dim 64, "
-                   "vocab 151936, tied embeddings), random bf16 weights N(0, 0.02^2)"),
+                   "vocab 151936, tied embeddings), random {dtype} weights N(0, 0.02^2)"),
 }
 
 
-def random_model(kind, device, seed=1):
-    """A causal LM of one of MODELS' shapes with bf16 random weights:
+WEIGHT_DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def random_model(kind, device, dtype=torch.bfloat16, seed=1):
+    """A causal LM of one of MODELS' shapes with random weights in `dtype`:
     matrices N(0, 0.02^2) (0.1 % replaced by 0.02 * Student-t(3) where the
     shape asks for outliers), norms 1, biases 0."""
     import transformers
     config_name, shape, outliers, _, _, _ = MODELS[kind]
-    config = getattr(transformers, config_name)(**shape, torch_dtype=torch.bfloat16)
+    config = getattr(transformers, config_name)(**shape, torch_dtype=dtype)
     with torch.device("meta"):
         model = transformers.AutoModelForCausalLM.from_config(config)
-    model = model.to(torch.bfloat16).to_empty(device=device)   # bf16 from the start: 70B fits
+    model = model.to(dtype).to_empty(device=device)   # in `dtype` from the start: 70B fits
     g = torch.Generator(device=device).manual_seed(seed)
     t_dist = torch.distributions.StudentT(torch.tensor(3.0, device=device))
     with torch.no_grad():
@@ -160,7 +163,7 @@ def random_model(kind, device, seed=1):
                 mask = torch.rand(p.shape, generator=g, device=device) < 0.001
                 w[mask] = (0.02 * t_dist.sample((int(mask.sum()),))).float()
                 del mask
-            p.copy_(w.to(torch.bfloat16))
+            p.copy_(w.to(dtype))
             del w
         # buffers were created uninitialized; the rotary frequencies stay fp32
         head = shape["hidden_size"] // shape["num_attention_heads"]
@@ -189,7 +192,7 @@ def time_generate(model, ids, new_tokens):
 
 def model_benchmark(args):
     """tok/s of greedy generation on a model shape of MODELS, NeuralZip
-    runtime against the same model uncompressed in bf16, with the prompt's
+    runtime against the same model uncompressed (bf16 or fp16), with the prompt's
     logits and every generated token compared bit for bit."""
     from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
     from neuralzip_amd.setup import NeuralZipSetup
@@ -198,7 +201,9 @@ def model_benchmark(args):
     prompt = args.prompt or default_prompt
     new_tokens = args.new_tokens or default_new
     t0 = time.perf_counter()
-    model = random_model(args.model, device)
+    dtype = WEIGHT_DTYPES[args.dtype]
+    description = description.format(dtype=args.dtype)
+    model = random_model(args.model, device, dtype)
     log(f"model built in {time.perf_counter() - t0:.1f}s")
     ids = torch.randint(0, shape["vocab_size"], (args.batch, prompt),
                         generator=torch.Generator().manual_seed(3)).to(device)
@@ -207,7 +212,7 @@ def model_benchmark(args):
     torch.cuda.reset_peak_memory_stats(device)
     base_s, base_out = time_generate(model, ids, new_tokens)
     base_peak = torch.cuda.max_memory_allocated(device)
-    log(f"bf16: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {base_peak / 2**30:.1f} GiB")
+    log(f"{args.dtype}: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {base_peak / 2**30:.1f} GiB")
     t0 = time.perf_counter()
     # setup and export read each weight back from the device one at a time
     marks = {}
@@ -250,7 +255,7 @@ def model_benchmark(args):
     tok_s = args.batch * steps / nz_s
     base_tok_s = args.batch * steps / base_s
     line = {
-        "metric": f"tok/s {args.model} shape bs={args.batch} vs uncompressed bf16",
+        "metric": f"tok/s {args.model} shape bs={args.batch} vs uncompressed {args.dtype}",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -260,7 +265,7 @@ def model_benchmark(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic",
         "config": {"workload": f"{description}, greedy generation, batch {args.batch}, {prompt} prompt + "
                                f"{new_tokens} new tokens, decode phase timed",
@@ -269,12 +274,12 @@ def model_benchmark(args):
                    "full_decode_pass_gbps": round(decoded_bytes / pass_ms / 1e6, 1),
                    "decoded_bytes_per_pass": int(decoded_bytes),
                    "compressed_store_bytes": int(runtime.store.nbytes),
-                   "peak_allocated_bf16_gib": round(base_peak / 2**30, 2),
+                   "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
                    "prefetch": runtime.prefetch},
-        "bf16_tok_s": round(base_tok_s, 2),
-        "ratio_vs_bf16": round(base_tok_s / tok_s, 3),
+        "uncompressed_tok_s": round(base_tok_s, 2),
+        "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
         "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
     }
@@ -294,7 +299,9 @@ def main():
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain 1 GiB device copy (calibrates HBM byte counters)")
     parser.add_argument("--model", choices=sorted(MODELS), default=None,
-                        help="model-level tok/s against uncompressed bf16 instead of the kernel benchmark")
+                        help="model-level tok/s against the uncompressed model instead of the kernel benchmark")
+    parser.add_argument("--dtype", choices=sorted(WEIGHT_DTYPES), default="bf16",
+                        help="weight dtype of the model benchmark")
     parser.add_argument("--batch", type=int, default=1)
     parser.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the model's)")
     parser.add_argument("--new-tokens", type=int, default=None, help="generated tokens (default: the model's)")

@@ -46,6 +46,15 @@ class DTypeSpec:
             exponent = (values << unsigned(1)) & unsigned(self.exponent_mask << (self.mantissa_bits + 1))
         return (sign | exponent | mantissa).astype(self.numpy, copy=False).tobytes()
 
+    def selected_lane(self, raw_bytes):
+        """The selected byte lane of the reordered words, without reordering
+        the whole buffer. With the sign moved below the exponent, the
+        exponent field fills that lane exactly (bfloat16 bits 7-14 land on
+        bits 8-15, float32 bits 23-30 on bits 24-31)."""
+        if self.bit_reorder:
+            return self.extract_exponents(raw_bytes).astype(np.uint8)
+        return np.frombuffer(raw_bytes, dtype=np.uint8)[self.selected_stream::self.element_size]
+
     def extract_exponents(self, raw_bytes):
         """Exponent fields of the original words."""
         values = np.frombuffer(raw_bytes, dtype=self.numpy)

@@ -117,8 +117,9 @@ class NeuralZipSetup:
             spec = DTYPES[tensor.dtype]
             raw = _tensor_raw_bytes(tensor)
             stream_id = spec.selected_stream
-            stream = np.frombuffer(spec.reorder_bytes(raw), dtype=np.uint8)[stream_id::spec.element_size]
-            exponents = spec.extract_exponents(raw)
+            stream = spec.selected_lane(raw)
+            # with the reorder, the selected lane is the exponent field itself
+            exponents = stream if spec.bit_reorder else spec.extract_exponents(raw)
             step = _stream_chunk_size(self.chunk_size, spec.element_size)
             key = (str(name), spec.name, stream_id)
             parents[key] = np.bincount(stream, minlength=256).astype(np.uint64)

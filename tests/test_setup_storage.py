@@ -89,3 +89,18 @@ def test_jensen_shannon_matches_scipy():
         p[rng.integers(0, 256, 30)] = 0
         p /= p.sum()
         assert abs(jensen_shannon_distance(p, q) - jensenshannon(p, q, base=2)) < 1e-12
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_selected_lane_is_the_reordered_lane(dtype):
+    """The clustering reads the selected lane directly; it must equal that lane
+    of the fully reordered words (every bf16/fp16 pattern, random fp32 ones)."""
+    from neuralzip_amd.dtypes import DTYPES
+    spec = DTYPES[dtype]
+    if spec.element_size == 2:
+        raw = np.arange(1 << 16, dtype=np.uint16).tobytes()
+    else:
+        raw = np.random.default_rng(3).integers(0, 1 << 32, 1 << 16, dtype=np.uint32).tobytes()
+    reordered = np.frombuffer(spec.reorder_bytes(raw), dtype=np.uint8)
+    expected = reordered[spec.selected_stream::spec.element_size]
+    assert np.array_equal(spec.selected_lane(raw), expected)
