@@ -9,7 +9,8 @@
  *   - every buffer is caller-owned; the library never frees caller memory;
  *   - int results: 0 on success, a negative nz_status on failure, with a
  *     thread-local message from nz_last_error();
- *   - host functions are re-entrant; nz_decode_launch is asynchronous and
+ *   - host functions are re-entrant; nz_decode_launch, nz_matvec_launch and
+ *     nz_matvec_reduce are asynchronous and
  *     ordered on the given HIP stream.
  */
 #ifndef NEURALZIP_HIP_H
@@ -22,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 2
+#define NZ_ABI_VERSION 3
 
 enum nz_status {
     NZ_OK = 0,
@@ -155,6 +156,47 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
 int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
                       const nz_work* segments, uint32_t n_segments, int element_size, int bit_reorder,
                       uint8_t* out);
+
+/* ---- fused decode and matrix-vector product ---------------------------- */
+
+/* At most this many activation rows per fused product. */
+#define NZ_MATVEC_MAX_BATCH 4
+
+/* Row index of a fused product y = x W^T + bias over one weight W (rows x
+ * cols, row-major) whose elements occupy workspace indices
+ * [weight_offset, weight_offset + rows * cols) of the tiles in `tiles`
+ * (n_tiles of them, in launch order). Every element must be covered by
+ * exactly one tile and each tile may touch at most two rows (cols of at
+ * least 2048 guarantees it); weight_offset and cols must be multiples of
+ * 16 / element_size. Writes row_index[rows + 1] and
+ * entries[row_index[n] .. row_index[n + 1]) = 2 * tile + slot (slot 1 when
+ * the tile started in the previous row), in element order. entries needs
+ * room for 2 * n_tiles values; *n_entries receives the count.
+ * No counterpart in the reference, which decodes a block into its workspace
+ * before the module's own GEMM reads it (gpu/inference.py:379-509). */
+int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
+                   uint32_t rows, uint32_t cols, int element_size, uint32_t* row_index, uint32_t* entries,
+                   uint32_t capacity, uint32_t* n_entries);
+
+/* Fused decode and product, first pass: for every tile t of the segments
+ * (a plan of nz_plan_work over the same tiles), the products of its
+ * elements with x (device, batch x cols in the weight's dtype, 1 <= batch
+ * <= NZ_MATVEC_MAX_BATCH) summed per row they touch, in
+ * partials[(2 * t + slot) * batch + b] (device fp32, 2 * n_tiles * batch
+ * values). One call per codebook kind (long_codes) of the weight's tiles.
+ * Asynchronous on `stream`. No counterpart in the reference (see
+ * nz_matvec_plan). */
+int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
+                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes, uint64_t weight_offset,
+                     uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream);
+
+/* Second pass: y[b * rows + n] = (sum of row n's partials, in entry order)
+ * + bias[n], rounded once to the weight's dtype. row_index and entries are
+ * device copies of nz_matvec_plan's output; bias (device, rows values in the
+ * weight's dtype) may be NULL. Asynchronous on `stream`. No counterpart in
+ * the reference (see nz_matvec_plan). */
+int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows, const float* partials,
+                     uint32_t batch, int element_size, int bit_reorder, const void* bias, void* y, void* stream);
 
 /* ---- storage format (host codecs) -------------------------------------- */
 

@@ -14,7 +14,7 @@ ARCH = os.environ.get("NZ_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HOST_SOURCES = ("codebook.cpp", "layout.cpp", "codec.cpp", "capi.cpp", "capi_storage.cpp")
-DEVICE_SOURCES = ("hip/decode_gfx950.hip",)
+DEVICE_SOURCES = ("hip/decode_gfx950.hip", "hip/matvec_gfx950.hip")
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", str(CSRC), "-I", str(ROOT / "include")]
 # packed FP32 instructions stay disabled on every HIP translation unit
 DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -40,6 +40,14 @@ extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const v
                                     void* stream, char* message, size_t message_size);
 extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_codes, int* out, char* message,
                                    size_t message_size);
+extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
+                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
+                                    uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch,
+                                    float* partials, uint32_t n_tiles, void* stream, char* message,
+                                    size_t message_size);
+extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows,
+                                    const float* partials, uint32_t batch, int element_size, int bit_reorder,
+                                    const void* bias, void* y, void* stream, char* message, size_t message_size);
 
 extern "C" {
 
@@ -201,6 +209,50 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
     char message[256] = {0};
     const int rc = nz_hip_decode_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
                                         long_codes, out, stream, message, sizeof message);
+    if (rc) return set_error(rc, message);
+    return 0;
+}
+
+int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
+                   uint32_t rows, uint32_t cols, int element_size, uint32_t* row_index, uint32_t* entries,
+                   uint32_t capacity, uint32_t* n_entries) {
+    return guarded([&] {
+        if (!frags || (!tiles && n_tiles) || !row_index || !entries || !n_entries)
+            nz::fail(nz::kInvalidArgument, "Null matvec plan argument.");
+        if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
+        std::vector<uint32_t> index, list;
+        nz::plan_matvec(frags, tiles, n_tiles, weight_offset, rows, cols, static_cast<unsigned>(element_size), index,
+                        list);
+        if (list.size() > capacity) nz::fail(nz::kInvalidArgument, "Entry buffer is too small.");
+        std::copy(index.begin(), index.end(), row_index);
+        std::copy(list.begin(), list.end(), entries);
+        *n_entries = static_cast<uint32_t>(list.size());
+    });
+}
+
+int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
+                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes, uint64_t weight_offset,
+                     uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream) {
+    if (n_segments && (!base || !frags || !tiles || !segments || !x || !partials))
+        return set_error(nz::kInvalidArgument, "Null matvec argument.");
+    if (cols == 0 || static_cast<uint64_t>(batch) * cols * static_cast<uint64_t>(element_size) > 0xFFFFFFFFull)
+        return set_error(nz::kInvalidArgument, "Activation rows exceed the addressable range.");
+    char message[256] = {0};
+    const int rc = nz_hip_matvec_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
+                                        long_codes, weight_offset, cols, x, batch, partials, n_tiles, stream, message,
+                                        sizeof message);
+    if (rc) return set_error(rc, message);
+    return 0;
+}
+
+int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows, const float* partials,
+                     uint32_t batch, int element_size, int bit_reorder, const void* bias, void* y, void* stream) {
+    if (rows && (!row_index || !entries || !partials || !y))
+        return set_error(nz::kInvalidArgument, "Null matvec reduce argument.");
+    if (batch > NZ_MATVEC_MAX_BATCH) return set_error(nz::kInvalidArgument, "matvec batch exceeds the maximum.");
+    char message[256] = {0};
+    const int rc = nz_hip_matvec_reduce(row_index, entries, rows, partials, batch, element_size, bit_reorder, bias,
+                                        y, stream, message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }

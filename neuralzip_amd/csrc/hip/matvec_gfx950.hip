@@ -1,0 +1,458 @@
+// matvec_gfx950.hip -- fused decode and matrix-vector product for gfx950.
+//
+// y[b, n] = sum_k W[n, k] * x[b, k] + bias[n] for a row-major weight W
+// (rows x cols) stored in the layout of nz_format.h, without writing W
+// anywhere. No counterpart in the reference, which always decodes a block
+// into its workspace before the module's own GEMM reads it
+// (neuralzip/gpu/inference.py:379-509).
+//
+//   * nz_matvec_kernel: the decode kernel's work split (one workgroup per
+//     segment of one codebook, LUT staged in LDS, wavefronts claiming tiles)
+//     and tile decode (tile_decode.h). Instead of storing the merged words, a
+//     wavefront multiplies them by the activations with v_dot2 (products
+//     accumulated in fp32) and reduces its lanes with DPP. A tile holds at
+//     most 2048 elements, so with cols >= 2048 it touches at most two rows;
+//     the wavefront writes one partial sum per (row slot, activation row).
+//   * nz_matvec_reduce_kernel: one thread per output row adds the row's
+//     partial sums in element order (a host-built CSR index), adds the bias
+//     in fp32 and rounds once to the weight's dtype.
+// Both kernels fix the order of every addition, so repeated calls give
+// identical bits.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../nz_format.h"
+#include "neuralzip_hip.h"
+#include "tile_decode.h"
+
+namespace {
+
+constexpr int kMatvecWaves = 16;
+constexpr int kMatvecThreads = kMatvecWaves * NZ_WAVE;
+constexpr int kReduceThreads = 256;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// One 16-byte vector of activations. The elements are copied out of the
+// load's ext-vector result one by one: clang lowers a __builtin_bit_cast of an
+// ext-vector element (v.y) to a read of element 0, so the bit casts below
+// only ever see the fields of a uint4.
+__device__ __forceinline__ uint4 load_vector(rsrc_t r, uint32_t offset) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+    return uint4{v.x, v.y, v.z, v.w};
+}
+
+// fp32 accumulation of the products of one 16-byte vector of weights and one
+// of activations (V elements each, in the weight's dtype).
+template <int ES, bool REORDER>
+__device__ __forceinline__ float dot_vector(const uint4& w, const uint4& x, float acc) {
+    if (ES == 2 && REORDER) {
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.x), __builtin_bit_cast(bf16x2, x.x), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.y), __builtin_bit_cast(bf16x2, x.y), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.z), __builtin_bit_cast(bf16x2, x.z), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.w), __builtin_bit_cast(bf16x2, x.w), acc, false);
+    } else if (ES == 2) {
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.x), __builtin_bit_cast(f16x2, x.x), acc, false);
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.y), __builtin_bit_cast(f16x2, x.y), acc, false);
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.z), __builtin_bit_cast(f16x2, x.z), acc, false);
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w.w), __builtin_bit_cast(f16x2, x.w), acc, false);
+    } else {
+        acc = __builtin_fmaf(__uint_as_float(w.x), __uint_as_float(x.x), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.y), __uint_as_float(x.y), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.z), __uint_as_float(x.z), acc);
+        acc = __builtin_fmaf(__uint_as_float(w.w), __uint_as_float(x.w), acc);
+    }
+    return acc;
+}
+
+// One element's word (in the low ES bytes of `v`) as fp32.
+template <int ES, bool REORDER>
+__device__ __forceinline__ float word_to_float(uint32_t v) {
+    if (ES == 2 && REORDER) return __uint_as_float(v << 16);
+    if (ES == 2) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
+    return __uint_as_float(v);
+}
+
+// Sum over the wavefront's 64 lanes, valid in lane 63 (the inclusive scan's
+// last element; the order of the additions is fixed).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+// Where a tile sits in the weight: staging index i holds element
+// (row0 + (i >= split), col0 + i - (i >= split ? cols : 0)).
+struct RowSpan {
+    uint32_t row0;
+    uint32_t col0;
+    uint32_t split;   // staging index of the next row's first element
+};
+
+__device__ __forceinline__ RowSpan row_span(uint64_t first, uint64_t weight_offset, uint32_t cols) {
+    const uint32_t rel = static_cast<uint32_t>(first - weight_offset);
+    RowSpan s;
+    s.row0 = rel / cols;
+    s.col0 = rel - s.row0 * cols;
+    s.split = cols - s.col0;
+    return s;
+}
+
+// The per-tile accumulators: acc[slot][b], slot 0 = row0, slot 1 = row0 + 1.
+template <int BT>
+struct Partial {
+    float acc[2][BT];
+    __device__ __forceinline__ void clear() {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int b = 0; b < BT; ++b) acc[s][b] = 0.0f;
+    }
+    // Reduces over the wavefront; lane 63 writes the 2 x batch sums of tile
+    // `t` (every other lane's stores fall outside the buffer range).
+    __device__ __forceinline__ void flush(rsrc_t partials, uint32_t t, uint32_t batch, uint32_t lane) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+                const float total = wave_sum(acc[s][b]);
+                const uint32_t at = ((2 * t + s) * batch + b) * 4u;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(total), partials,
+                                                      lane == NZ_WAVE - 1 && b < static_cast<int>(batch) ? at : kOutOfRange,
+                                                      0, 0);
+            }
+    }
+};
+
+// Adds the products of a tile's staged elements (Huffman tiles) to `p`.
+template <int ES, bool REORDER, bool LONG, int BT>
+__device__ __forceinline__ void multiply_tile(const TileInfo& ti, const Fetch<ES, LONG>& d, const uint8_t* stage,
+                                              const RowSpan& rs, rsrc_t x, uint32_t cols, uint32_t batch,
+                                              uint32_t lane, Partial<BT>& p) {
+    using G = Geometry<ES>;
+    constexpr uint32_t V = G::V;
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+        // the activations of every round first, then one round's weights at a time
+        uint4 xv[G::kRounds];
+#pragma unroll
+        for (uint32_t r = 0; r < G::kRounds; ++r) {
+            const uint32_t g = (lane + NZ_WAVE * r) * V;
+            const bool whole = g >= ti.s0 && g + V <= ti.s1;
+            const uint32_t col = rs.col0 + g - (g >= rs.split ? cols : 0u);
+            xv[r] = load_vector(x, whole && b < static_cast<int>(batch) ? (b * cols + col) * ES : kOutOfRange);
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < G::kRounds; ++r) {
+            const uint32_t g = (lane + NZ_WAVE * r) * V;
+            const bool whole = g >= ti.s0 && g + V <= ti.s1;
+            const uint8_t* at = stage + NZ_STAGE_ORIGIN + (whole ? g : 0u);
+            uint32_t e0, e1 = 0;
+            if (ES == 2) {
+                const uint2 e = *reinterpret_cast<const uint2*>(at);
+                e0 = e.x;
+                e1 = e.y;
+            } else {
+                e0 = *reinterpret_cast<const uint32_t*>(at);
+            }
+            const uint4 v = merge_vector<ES, REORDER>(e0, e1, d.raw[r]);
+            // staged bytes outside the tile are stale: keep them out of the sums
+            const float dot = whole ? dot_vector<ES, REORDER>(v, xv[r], 0.0f) : 0.0f;
+            const bool hi = g >= rs.split;
+            p.acc[0][b] += hi ? 0.0f : dot;
+            p.acc[1][b] += hi ? dot : 0.0f;
+        }
+    }
+    if (ti.s0 != 0 || ti.s1 % V != 0) {   // elements of the partial first and last vectors (fragment ends)
+        const uint32_t g = edge_index<ES>(ti, lane);
+        const uint32_t vec0 = g & ~(V - 1);
+        const bool partial = !(vec0 >= ti.s0 && vec0 + V <= ti.s1);
+        const bool mine = lane < 2 * V && (lane < V || ti.nv > 1) && partial && g >= ti.s0 && g < ti.s1;
+        const uint32_t expo = stage[NZ_STAGE_ORIGIN + (mine ? g : 0u)];
+        const float wf = mine ? word_to_float<ES, REORDER>(restore_word<ES, REORDER>((expo << (8 * (ES - 1))) | d.edge))
+                              : 0.0f;
+        const bool h = g >= rs.split;
+        const uint32_t col = rs.col0 + g - (h ? cols : 0u);
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+            const uint32_t off = mine && b < static_cast<int>(batch) ? (b * cols + col) * ES : kOutOfRange;
+            const uint32_t xw = ES == 2 ? __builtin_amdgcn_raw_buffer_load_b16(x, off, 0, 0)
+                                        : __builtin_amdgcn_raw_buffer_load_b32(x, off, 0, 0);
+            const float prod = wf * word_to_float<ES, REORDER>(xw);
+            p.acc[0][b] += h ? 0.0f : prod;
+            p.acc[1][b] += h ? prod : 0.0f;
+        }
+    }
+    wave_lds_sync();   // the staging area is rewritten by the next tile
+}
+
+template <int ES, bool REORDER, bool LONG, bool ESC, int BT>
+__device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
+                                                const nz_work& seg, uint32_t* counter, uint32_t lane,
+                                                const uint32_t* lut, uint8_t* stage, uint64_t weight_offset,
+                                                uint32_t cols, rsrc_t x, uint32_t batch, rsrc_t partials) {
+    const uint32_t n = seg.tile1 - seg.tile0;
+    uint32_t t = claim(counter, lane);
+    if (t >= n) return;
+    TileInfo cur = tile_info<ES>(base, frags, tiles, seg.tile0 + t);
+    Fetch<ES, LONG> fc;
+    fetch<ES, LONG>(cur, lane, fc);
+    uint32_t tn = claim(counter, lane);
+    Partial<BT> p;
+    for (;;) {
+        const bool more = tn < n;
+        const TileInfo nxt = tile_info<ES>(base, frags, tiles, seg.tile0 + (more ? tn : t));
+        Fetch<ES, LONG> fn;
+        fetch<ES, LONG>(nxt, lane, fn);
+        const uint32_t after = more ? claim(counter, lane) : n;
+        stage_tile<ES, LONG, ESC>(cur, fc, lut, stage, lane);
+        p.clear();
+        multiply_tile<ES, REORDER, LONG, BT>(cur, fc, stage, row_span(cur.first, weight_offset, cols), x, cols, batch,
+                                             lane, p);
+        p.flush(partials, seg.tile0 + t, batch, lane);
+        if (!more) break;
+        t = tn;
+        tn = after;
+        cur = nxt;
+        fc = fn;
+    }
+}
+
+// A raw (uncoded) tile: the exponent lane is stored as is.
+template <int ES, bool REORDER, int BT>
+__device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f, const nz_tile& tile,
+                         uint64_t weight_offset, uint32_t cols, rsrc_t x, uint32_t batch, uint32_t lane,
+                         Partial<BT>& p) {
+    constexpr uint32_t V = 16 / ES;
+    const uint64_t A0 = f.out + tile.out0, A1 = A0 + nz_tile_elements(tile.counts);
+    const uint64_t first = A0 / V * V;
+    const uint32_t s0 = static_cast<uint32_t>(A0 - first), s1 = static_cast<uint32_t>(A1 - first);
+    const uint32_t nv = (s1 + V - 1) / V;
+    const uint64_t origin = f.out / V * V;
+    const RowSpan rs = row_span(first, weight_offset, cols);
+    for (uint32_t i = lane; i < nv; i += NZ_WAVE) {
+        const uint32_t g = i * V;
+        const uint8_t* expo = base + f.bits + (first + g - origin);
+        const uint8_t* lanes = base + f.lanes + (first + g - origin);
+        if (g >= s0 && g + V <= s1) {
+            uint32_t e0, e1 = 0, r[3];
+            if (ES == 2) {
+                const uint2 e = *reinterpret_cast<const uint2*>(expo);
+                e0 = e.x;
+                e1 = e.y;
+                const uint2 l = *reinterpret_cast<const uint2*>(lanes);
+                r[0] = l.x;
+                r[1] = l.y;
+            } else {
+                e0 = *reinterpret_cast<const uint32_t*>(expo);
+                r[0] = *reinterpret_cast<const uint32_t*>(lanes);
+                r[1] = *reinterpret_cast<const uint32_t*>(lanes + f.lane_stride);
+                r[2] = *reinterpret_cast<const uint32_t*>(lanes + 2 * f.lane_stride);
+            }
+            const uint4 w = merge_vector<ES, REORDER>(e0, e1, r);
+            const bool h = g >= rs.split;
+            const uint32_t col = rs.col0 + g - (h ? cols : 0u);
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+                const uint4 xv = load_vector(x, b < static_cast<int>(batch) ? (b * cols + col) * ES : kOutOfRange);
+                const float dot = dot_vector<ES, REORDER>(w, xv, 0.0f);
+                p.acc[0][b] += h ? 0.0f : dot;
+                p.acc[1][b] += h ? dot : 0.0f;
+            }
+        } else {
+            for (uint32_t j = 0; j < V; ++j) {
+                if (g + j < s0 || g + j >= s1) continue;
+                uint32_t raw = 0;
+                for (int k = 0; k + 1 < ES; ++k) raw |= static_cast<uint32_t>(lanes[j + k * f.lane_stride]) << (8 * k);
+                const float wf =
+                    word_to_float<ES, REORDER>(restore_word<ES, REORDER>((static_cast<uint32_t>(expo[j]) << (8 * (ES - 1))) | raw));
+                const bool h = g + j >= rs.split;
+                const uint32_t col = rs.col0 + g + j - (h ? cols : 0u);
+#pragma unroll
+                for (int b = 0; b < BT; ++b) {
+                    const uint32_t off = b < static_cast<int>(batch) ? (b * cols + col) * ES : kOutOfRange;
+                    const uint32_t xw = ES == 2 ? __builtin_amdgcn_raw_buffer_load_b16(x, off, 0, 0)
+                                                : __builtin_amdgcn_raw_buffer_load_b32(x, off, 0, 0);
+                    const float prod = wf * word_to_float<ES, REORDER>(xw);
+                    p.acc[0][b] += h ? 0.0f : prod;
+                    p.acc[1][b] += h ? prod : 0.0f;
+                }
+            }
+        }
+    }
+}
+
+template <int ES, bool REORDER, bool LONG, int BT>
+__global__ __launch_bounds__(kMatvecThreads) __attribute__((amdgpu_waves_per_eu(8)))
+void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
+                      const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs, uint64_t weight_offset,
+                      uint32_t cols, const uint8_t* __restrict__ xp, uint32_t batch, float* __restrict__ partials_p,
+                      uint32_t n_tiles) {
+    using G = Geometry<ES>;
+    __shared__ __align__(16) uint32_t s_lut[NZ_LUT_MAX_WORDS];
+    __shared__ __align__(16) uint8_t s_stage[kMatvecWaves][G::kStage];
+    __shared__ uint32_t s_claim;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / NZ_WAVE);
+    const uint32_t lane = threadIdx.x % NZ_WAVE;
+    const nz_work seg = segs[blockIdx.x];
+    const rsrc_t x = make_rsrc(xp, batch * cols * ES);
+    const rsrc_t partials = make_rsrc(partials_p, n_tiles * 2u * batch * 4u);
+    if (threadIdx.x == 0) s_claim = 0;
+    if (seg.kind == NZ_KIND_RAW) {
+        __syncthreads();
+        const uint32_t n = seg.tile1 - seg.tile0;
+        Partial<BT> p;
+        for (uint32_t t = claim(&s_claim, lane); t < n; t = claim(&s_claim, lane)) {
+            const nz_tile tile = tiles[seg.tile0 + t];
+            p.clear();
+            raw_tile<ES, REORDER, BT>(base, frags[tile.frag], tile, weight_offset, cols, x, batch, lane, p);
+            p.flush(partials, seg.tile0 + t, batch, lane);
+        }
+        return;
+    }
+    const uint4* img = reinterpret_cast<const uint4*>(base + frags[seg.lut_frag].lut);
+    const uint32_t words = reinterpret_cast<const uint32_t*>(img)[2];
+    uint4* dst = reinterpret_cast<uint4*>(s_lut);
+    for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kMatvecThreads) dst[i] = img[i];
+    __syncthreads();
+    if constexpr (LONG) {
+        huffman_segment<ES, REORDER, true, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave],
+                                                     weight_offset, cols, x, batch, partials);
+    } else {
+        if (s_lut[0])
+            huffman_segment<ES, REORDER, false, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut,
+                                                          s_stage[wave], weight_offset, cols, x, batch, partials);
+        else
+            huffman_segment<ES, REORDER, false, false, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut,
+                                                           s_stage[wave], weight_offset, cols, x, batch, partials);
+    }
+}
+
+// fp32 to the weight's dtype, rounding to nearest even.
+template <int ES, bool REORDER>
+__device__ __forceinline__ void store_result(uint8_t* y, uint32_t index, float v) {
+    if (ES == 2 && REORDER) {
+        const uint32_t u = __float_as_uint(v);
+        const uint32_t r = (u & 0x7FFFFFFFu) > 0x7F800000u ? (u >> 16) | 0x40u   // NaN stays NaN
+                                                           : (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+        reinterpret_cast<uint16_t*>(y)[index] = static_cast<uint16_t>(r);
+    } else if (ES == 2) {
+        reinterpret_cast<_Float16*>(y)[index] = static_cast<_Float16>(v);
+    } else {
+        reinterpret_cast<float*>(y)[index] = v;
+    }
+}
+
+template <int ES, bool REORDER>
+__global__ __launch_bounds__(kReduceThreads)
+void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint32_t* __restrict__ entries,
+                             uint32_t rows, const float* __restrict__ partials, uint32_t batch,
+                             const uint8_t* __restrict__ bias, uint8_t* __restrict__ y) {
+    const uint32_t n = blockIdx.x * kReduceThreads + threadIdx.x;
+    if (n >= rows) return;
+    const uint32_t e0 = row_index[n], e1 = row_index[n + 1];
+    const float add = bias == nullptr ? 0.0f
+                      : word_to_float<ES, REORDER>(ES == 2 ? reinterpret_cast<const uint16_t*>(bias)[n]
+                                                           : reinterpret_cast<const uint32_t*>(bias)[n]);
+    for (uint32_t b = 0; b < batch; ++b) {
+        float sum = 0.0f;
+        for (uint32_t e = e0; e < e1; ++e) sum += partials[entries[e] * batch + b];
+        store_result<ES, REORDER>(y, b * rows + n, sum + add);
+    }
+}
+
+template <int ES, bool REORDER, bool LONG, int BT>
+hipError_t launch_matvec(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
+                         uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch, float* partials,
+                         uint32_t n_tiles, hipStream_t stream) {
+    hipLaunchKernelGGL((nz_matvec_kernel<ES, REORDER, LONG, BT>), dim3(n_segs), dim3(kMatvecThreads), 0, stream,
+                       static_cast<const uint8_t*>(base), static_cast<const nz_frag_desc*>(frags),
+                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs), weight_offset, cols,
+                       static_cast<const uint8_t*>(x), batch, partials, n_tiles);
+    return hipGetLastError();
+}
+
+template <int ES, bool REORDER, bool LONG>
+hipError_t launch_batch(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
+                        uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch, float* partials,
+                        uint32_t n_tiles, hipStream_t stream) {
+#define NZ_MATVEC(BT) \
+    launch_matvec<ES, REORDER, LONG, BT>(base, frags, tiles, segs, n_segs, weight_offset, cols, x, batch, partials, n_tiles, stream)
+    if (batch <= 1) return NZ_MATVEC(1);
+    if (batch <= 2) return NZ_MATVEC(2);
+    return NZ_MATVEC(4);
+#undef NZ_MATVEC
+}
+
+bool layout_ok(int element_size, int bit_reorder, char* message, size_t message_size) {
+    if ((element_size == 2) || (element_size == 4 && bit_reorder)) return true;
+    snprintf(message, message_size, "Unsupported GPU layout (element_size=%d, bit_reorder=%d).", element_size,
+             bit_reorder);
+    return false;
+}
+
+}  // namespace
+
+// Partial sums of one launch (one codebook kind) of a weight's tiles: writes
+// partials[(2 * t + slot) * batch + b] for every tile t the segments cover.
+extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
+                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
+                                    uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch,
+                                    float* partials, uint32_t n_tiles, void* stream, char* message,
+                                    size_t message_size) {
+    if (n_segs == 0) return 0;
+    if (!layout_ok(element_size, bit_reorder, message, message_size)) return -1;
+    if (batch == 0 || batch > NZ_MATVEC_MAX_BATCH) {
+        snprintf(message, message_size, "matvec batch must be in [1, %d] (got %u).", NZ_MATVEC_MAX_BATCH, batch);
+        return -1;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t rc;
+#define NZ_BATCH(E, R, L) launch_batch<E, R, L>(base, frags, tiles, segs, n_segs, weight_offset, cols, x, batch, partials, n_tiles, st)
+    if (element_size == 2 && bit_reorder)
+        rc = long_codes ? NZ_BATCH(2, true, true) : NZ_BATCH(2, true, false);
+    else if (element_size == 2)
+        rc = long_codes ? NZ_BATCH(2, false, true) : NZ_BATCH(2, false, false);
+    else
+        rc = long_codes ? NZ_BATCH(4, true, true) : NZ_BATCH(4, true, false);
+#undef NZ_BATCH
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "matvec launch failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    return 0;
+}
+
+// y[b * rows + n] = sum of row n's partial sums (+ bias[n]), in the weight's dtype.
+extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows,
+                                    const float* partials, uint32_t batch, int element_size, int bit_reorder,
+                                    const void* bias, void* y, void* stream, char* message, size_t message_size) {
+    if (rows == 0 || batch == 0) return 0;
+    if (!layout_ok(element_size, bit_reorder, message, message_size)) return -1;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((rows + kReduceThreads - 1) / kReduceThreads);
+    const uint8_t* b = static_cast<const uint8_t*>(bias);
+    uint8_t* out = static_cast<uint8_t*>(y);
+    if (element_size == 2 && bit_reorder)
+        hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, true>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
+                           rows, partials, batch, b, out);
+    else if (element_size == 2)
+        hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, false>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
+                           rows, partials, batch, b, out);
+    else
+        hipLaunchKernelGGL((nz_matvec_reduce_kernel<4, true>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
+                           rows, partials, batch, b, out);
+    const hipError_t rc = hipGetLastError();
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "matvec reduce launch failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    return 0;
+}

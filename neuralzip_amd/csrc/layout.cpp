@@ -4,6 +4,7 @@
 // Replaces the reference's GPU layout encoder (gpu_layout.h:62-241) and the
 // launcher's descriptor construction (decoder.py:130-191).
 #include "layout.hpp"
+#include "neuralzip_hip.h"
 
 #include <algorithm>
 #include <cstring>
@@ -208,6 +209,54 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 }
 
 constexpr uint64_t kMinTilesPerGroup = 16;
+
+void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
+                 uint32_t rows, uint32_t cols, unsigned element_size, std::vector<uint32_t>& row_index,
+                 std::vector<uint32_t>& entries) {
+    if (element_size != 2 && element_size != 4) fail(kInvalidArgument, "element_size must be 2 or 4.");
+    const uint32_t V = 16 / element_size;
+    if (!rows || !cols) fail(kInvalidArgument, "The weight has no elements.");
+    if (cols % V || weight_offset % V)
+        fail(kInvalidArgument, "Weight offset and row length must be multiples of 16 bytes of elements.");
+    const uint64_t numel = static_cast<uint64_t>(rows) * cols;
+    if (numel > 0xFFFFFFFFull) fail(kLayoutLimit, "The weight exceeds 2^32 elements.");
+    if (static_cast<uint64_t>(n_tiles) * 2 > 0xFFFFFFFFull / (4 * NZ_MATVEC_MAX_BATCH))
+        fail(kLayoutLimit, "Too many tiles for one product.");
+    struct Span {
+        uint64_t a0, a1;
+        uint32_t tile;
+    };
+    std::vector<Span> spans(n_tiles);
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const nz_frag_desc& f = frags[tiles[t].frag];
+        const uint64_t a0 = f.out + tiles[t].out0;
+        const uint64_t a1 = a0 + nz_tile_elements(tiles[t].counts);
+        if (a0 < weight_offset || a1 > weight_offset + numel || a1 <= a0)
+            fail(kInvalidArgument, "A tile lies outside the weight.");
+        spans[t] = {a0 - weight_offset, a1 - weight_offset, t};
+    }
+    std::sort(spans.begin(), spans.end(), [](const Span& a, const Span& b) { return a.a0 < b.a0; });
+    uint64_t cursor = 0;
+    for (const Span& s : spans) {
+        if (s.a0 != cursor) fail(kInvalidArgument, "The tiles do not cover the weight exactly once.");
+        if ((s.a1 - 1) / cols - s.a0 / cols > 1) fail(kLayoutLimit, "A tile spans more than two rows.");
+        cursor = s.a1;
+    }
+    if (cursor != numel) fail(kInvalidArgument, "The tiles do not cover the weight exactly once.");
+    // spans are in element order, so each row's entries are appended in order
+    row_index.assign(static_cast<size_t>(rows) + 1, 0);
+    entries.clear();
+    entries.reserve(static_cast<size_t>(n_tiles) + rows);
+    uint32_t row = 0;
+    for (const Span& s : spans) {
+        const uint32_t r0 = static_cast<uint32_t>(s.a0 / cols), r1 = static_cast<uint32_t>((s.a1 - 1) / cols);
+        for (uint32_t r = r0; r <= r1; ++r) {
+            while (row < r) row_index[++row] = static_cast<uint32_t>(entries.size());
+            entries.push_back(2 * s.tile + (r > r0 ? 1u : 0u));
+        }
+    }
+    while (row < rows) row_index[++row] = static_cast<uint32_t>(entries.size());
+}
 
 std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
     std::vector<nz_work> runs;   // maximal runs of one LUT and kind

@@ -150,6 +150,78 @@ class HIPDecoder:
                 cache[(device, key)] = _native.decode_slots(*key)
         return cache[(device, key)]
 
+    def prepare_matvec(self, store, fragment_indices, dtype, weight_offset, rows, cols, slots=SLOTS):
+        """Fused product over the weight (rows x cols, row-major, at workspace
+        element `weight_offset`) that `fragment_indices` encode. Raises
+        NativeError when the weight's tiles do not suit the fused kernel
+        (rows shorter than a tile, misaligned offsets)."""
+        fragment_indices = list(fragment_indices)
+        if not fragment_indices:
+            raise ValueError("A fused product needs at least one fragment.")
+        order = sorted(fragment_indices, key=lambda i: (int(store.descs[i]["kind"]), int(store.descs[i]["lut"]), i))
+        tiles = np.concatenate([store.fragment_tiles(i) for i in order])
+        row_index, entries = _native.matvec_plan(store.descs, tiles, weight_offset, rows, cols, dtype.element_size)
+        device = store.device
+        longs = [bool(store.descs[i]["kind"] == KIND_LONG) for i in fragment_indices]
+        key = (dtype.element_size, bool(dtype.bit_reorder), any(longs))
+        if slots is None:
+            slots = self.slots(device, key)
+        segments = _native.plan_work(store.descs, tiles, slots)
+        # one launch per kernel variant: segments of long-code fragments apart
+        is_long = segments["kind"] == KIND_LONG
+        groups = [segments[~is_long], segments[is_long]]
+        tensors = [torch.from_numpy(tiles.view(np.uint8).copy()).to(device),
+                   torch.from_numpy(row_index.view(np.uint8).copy()).to(device),
+                   torch.from_numpy(entries.view(np.uint8).copy()).to(device)]
+        launches = []
+        for long_codes, group in enumerate(groups):
+            if len(group):
+                t = torch.from_numpy(group.view(np.uint8).copy()).to(device)
+                tensors.append(t)
+                launches.append((t.data_ptr(), len(group), long_codes))
+        descs = store.descs[fragment_indices]
+        numel = descs["numel"].astype(np.int64)
+        raw = descs["kind"] == KIND_RAW
+        bits = np.where(raw, numel, (descs["bit_length"].astype(np.int64) + 7) // 8)
+        windows = np.where(raw, 0, (descs["bit_length"].astype(np.int64) + WINDOW_BITS - 1) // WINDOW_BITS)
+        reads = int(bits.sum() + 2 * windows.sum() + (numel * (dtype.element_size - 1)).sum())
+        return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, int(rows), int(cols), len(tiles),
+                              int(weight_offset), store, tuple(launches), reads)
+
+    def matvec(self, prepared, x, bias=None, partials=None, stream=None):
+        """y = x @ W^T (+ bias) for x of shape (batch, cols), batch <=
+        MATVEC_MAX_BATCH, in the weight's dtype; `partials` (fp32, at least
+        2 * n_tiles * batch values) is the scratch of the first pass. Returns
+        a new (batch, rows) tensor; ordered on `stream` (default: current)."""
+        batch = x.shape[0]
+        if x.dim() != 2 or x.shape[1] != prepared.cols or not 1 <= batch <= _native.MATVEC_MAX_BATCH:
+            raise ValueError(f"matvec input must be (1..{_native.MATVEC_MAX_BATCH}, {prepared.cols}); "
+                             f"got {tuple(x.shape)}.")
+        if x.dtype != prepared.dtype or x.device != prepared.device:
+            raise ValueError("matvec input must match the weight's dtype and device.")
+        if bias is not None and (bias.dtype != prepared.dtype or bias.numel() != prepared.rows):
+            raise ValueError("matvec bias must match the weight's dtype and rows.")
+        x = x.contiguous()
+        need = 2 * prepared.n_tiles * batch
+        if partials is None:
+            partials = torch.empty(need, dtype=torch.float32, device=prepared.device)
+        elif partials.dtype != torch.float32 or partials.numel() < need or partials.device != prepared.device:
+            raise ValueError("matvec partials buffer is too small.")
+        if stream is None:
+            stream = torch.cuda.current_stream(prepared.device)
+        y = torch.empty((batch, prepared.rows), dtype=prepared.dtype, device=prepared.device)
+        tiles_t, row_index_t, entries_t = prepared.device_tensors[:3]
+        es, reorder = prepared.layout
+        for segments_ptr, n_segments, long_codes in prepared.launches:
+            _native.matvec_launch(prepared.store.buffer.data_ptr(), prepared.store.frags.data_ptr(),
+                                  tiles_t.data_ptr(), segments_ptr, n_segments, es, int(reorder), long_codes,
+                                  prepared.weight_offset, prepared.cols, x.data_ptr(), batch, partials.data_ptr(),
+                                  prepared.n_tiles, stream.cuda_stream)
+        _native.matvec_reduce(row_index_t.data_ptr(), entries_t.data_ptr(), prepared.rows, partials.data_ptr(), batch,
+                              es, int(reorder), None if bias is None else bias.contiguous().data_ptr(), y.data_ptr(),
+                              stream.cuda_stream)
+        return y
+
     def decode_batch(self, prepared, stream=None):
         """Launches the batch on `stream` (default: the current stream); the
         batch holds its device arrays, so the saved pointers stay valid."""
@@ -157,6 +229,24 @@ class HIPDecoder:
             stream = torch.cuda.current_stream(prepared.device)
         _native.decode_launch(*prepared.launch_args, stream.cuda_stream)
         return prepared.outputs
+
+
+@dataclass(frozen=True)
+class PreparedMatvec:
+    """One weight's fused decode and matrix-vector product: its tiles, one
+    launch per codebook kind, and the row index of the partial sums."""
+    device_tensors: tuple = field(repr=False)          # tiles, segments, row index, entries on the device
+    device: torch.device
+    layout: tuple                                      # (element_size, bit_reorder)
+    dtype: torch.dtype
+    rows: int
+    cols: int
+    n_tiles: int
+    weight_offset: int
+    store: DeviceStore = field(repr=False)
+    # (segments pointer, count, long_codes) of each launch
+    launches: tuple = field(repr=False, default=())
+    algorithmic_bytes: int = 0
 
 
 def algorithmic_bytes(descs, dtype):

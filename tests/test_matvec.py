@@ -1,0 +1,210 @@
+"""Fused decode and matrix-vector product through the C ABI
+(nz_matvec_plan, nz_matvec_launch, nz_matvec_reduce).
+
+The fused product has no counterpart in the reference, which always decodes
+a block's weights before the module's own GEMM (gpu/inference.py:379-509).
+Its bar is the product of the exact weights: y is compared with
+x @ W^T + bias evaluated in float64 from the original words. The error
+allowed is fp32 accumulation over `cols` terms plus one rounding to the
+output dtype. Repeated calls must give identical bits. Every partial sum
+the reduction reads must have been written: the partials buffer is poisoned
+with NaN first.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from neuralzip_amd import _native
+from neuralzip_amd.dtypes import DTYPES
+from nz_helpers import Encoded, segment_lengths, singleton_header
+
+HALF_ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -24}
+
+
+def random_weight(dtype, rows, cols, seed, scale=0.02):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=g) * scale
+    outliers = torch.rand(rows, cols, generator=g) < 0.001
+    w[outliers] *= 20
+    return w.to(dtype)
+
+
+def mixed_header(raw, dtype, pairs=64):
+    """An NZM1 code with the lane's most frequent pairs (the setup's rule)."""
+    spec = DTYPES[dtype]
+    lanes = oracle.split_lanes(raw.tobytes(), spec.element_size, spec.bit_reorder, spec.mantissa_bits,
+                               spec.exponent_mask.bit_length())
+    lane = lanes[spec.selected_stream].astype(np.uint16)
+    counts = np.bincount(lane[:-1] | (lane[1:] << 8), minlength=65536)
+    top = np.sort(np.argsort(-counts, kind="stable")[:pairs]).astype("<u2")
+    vocab = top.tobytes()
+    tokens = oracle.count_mixed_tokens([lane.astype(np.uint8).tobytes()], vocab)
+    return oracle.build_mixed_codebook(tokens, vocab), vocab
+
+
+def long_code_weight(rows, cols, seed):
+    """bf16 words whose exponent bytes (118..127) all have 55- or 56-bit codes
+    under the segment code of segment_lengths(56); values are finite."""
+    rng = np.random.default_rng(seed)
+    n = rows * cols
+    exponent = rng.integers(118, 128, n).astype(np.uint16)
+    low = rng.integers(0, 256, n).astype(np.uint16)   # sign and mantissa after the reorder
+    reordered = (exponent << 8) | low
+    spec = DTYPES[torch.bfloat16]
+    words = np.frombuffer(spec.reorder_bytes(reordered.astype("<u2").tobytes(), restore=True), dtype="<u2")
+    return torch.from_numpy(words.astype(np.int16).copy()).view(torch.bfloat16).reshape(rows, cols)
+
+
+def tile_spans(descs, tiles, weight_offset):
+    a0 = descs["out"][tiles["frag"]].astype(np.int64) + tiles["out0"].astype(np.int64) - weight_offset
+    return a0, a0 + tiles["n_out"].astype(np.int64)
+
+
+def launch_order(descs, tiles):
+    """Tiles with those of one codebook and kind adjacent (the runtime's order)."""
+    key = np.lexsort((tiles["frag"], descs["lut"][tiles["frag"]], descs["kind"][tiles["frag"]]))
+    return tiles[key]
+
+
+def encoded_case(case, dtype, seed=1):
+    """(weight, Encoded, weight_offset): the weight at workspace offset 64."""
+    offset = 64
+    if case == "huff0":
+        w = random_weight(dtype, 37, 4096, seed)
+        raw = w.view(torch.uint8).numpy().reshape(-1).copy()
+        books = {0: _native.Codebook(singleton_header(raw, dtype))}
+        n = -(-w.numel() // 20000)
+        ids = [0] * n
+        ids[2] = -1                                   # one chunk stays raw
+        return w, Encoded([(raw, dtype, 20000, ids, offset)], books), offset
+    if case == "nzm1":
+        w = random_weight(dtype, 24, 14336, seed)
+        raw = w.view(torch.uint8).numpy().reshape(-1).copy()
+        header, vocab = mixed_header(raw, dtype)
+        books = {0: _native.Codebook(header, vocab), 1: _native.Codebook(singleton_header(raw, dtype))}
+        n = -(-w.numel() // 131072)
+        return w, Encoded([(raw, dtype, 131072, [i % 2 for i in range(n)], offset)], books), offset
+    if case == "long":
+        w = long_code_weight(16, 2048, seed)
+        raw = w.view(torch.uint8).numpy().reshape(-1).copy()
+        vocab = bytes((127, 127, 125, 126))
+        books = {0: _native.Codebook(b"NZM1" + segment_lengths(56), vocab),
+                 1: _native.Codebook(singleton_header(raw, torch.bfloat16))}
+        return w, Encoded([(raw, torch.bfloat16, 8192, [0, 1, 0, 1], offset)], books), offset
+    raise ValueError(case)
+
+
+# ---------------------------------------------------------------- host plan
+
+def test_plan_covers_each_row_in_element_order():
+    w, enc, offset = encoded_case("huff0", torch.bfloat16)
+    _, descs, tiles = enc.host_image()
+    tiles = launch_order(descs, tiles)
+    rows, cols = w.shape
+    row_index, entries = _native.matvec_plan(descs, tiles, offset, rows, cols, 2)
+    a0, a1 = tile_spans(descs, tiles, offset)
+    assert row_index[0] == 0 and row_index[-1] == len(entries)
+    for r in range(rows):
+        covered, last = 0, -1
+        for e in entries[row_index[r]:row_index[r + 1]]:
+            t, slot = int(e) // 2, int(e) % 2
+            lo, hi = max(a0[t], r * cols), min(a1[t], (r + 1) * cols)
+            assert lo < hi, "entry for a tile outside its row"
+            assert slot == int(a0[t] < r * cols)
+            assert lo > last
+            last = lo
+            covered += hi - lo
+        assert covered == cols
+
+
+def test_plan_refuses_what_the_kernel_cannot_reduce():
+    w, enc, offset = encoded_case("huff0", torch.bfloat16)
+    _, descs, tiles = enc.host_image()
+    rows, cols = w.shape
+    with pytest.raises(_native.NativeError, match="more than two rows"):
+        _native.matvec_plan(descs, tiles, offset, rows * 4, cols // 4, 2)     # 1024-element rows
+    with pytest.raises(_native.NativeError, match="exactly once"):
+        _native.matvec_plan(descs, np.delete(tiles, 5), offset, rows, cols, 2)
+    with pytest.raises(_native.NativeError, match="multiples"):
+        _native.matvec_plan(descs, tiles, offset + 4, rows, cols, 2)
+    with pytest.raises(_native.NativeError, match="outside"):
+        _native.matvec_plan(descs, tiles, offset, rows - 1, cols, 2)
+
+
+# ---------------------------------------------------------------- GPU parity
+
+def run_matvec(base, descs, tiles, dtype, weight_offset, rows, cols, x, bias=None, calls=2):
+    """y of `calls` consecutive calls (partials poisoned before each)."""
+    spec = DTYPES[dtype]
+    device = torch.device("cuda:0")
+    tiles = launch_order(descs, tiles)
+    row_index, entries = _native.matvec_plan(descs, tiles, weight_offset, rows, cols, spec.element_size)
+    segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
+    dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)
+    base_t, frags_t, tiles_t = dev(base), dev(descs), dev(tiles)
+    index_t, entries_t = dev(row_index), dev(entries)
+    launches = []
+    for long_codes in (0, 1):
+        sel = segments[(segments["kind"] == _native.KIND_LONG) == bool(long_codes)]
+        if len(sel):
+            launches.append((dev(sel), len(sel), long_codes))
+    batch = x.shape[0]
+    x_t = x.contiguous().to(device)
+    bias_t = None if bias is None else bias.to(device)
+    partials = torch.empty(2 * len(tiles) * batch, dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    outs = []
+    for _ in range(calls):
+        partials.fill_(float("nan"))
+        y = torch.full((batch, rows), float("nan"), dtype=dtype, device=device)
+        for seg_t, n, long_codes in launches:
+            _native.matvec_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), seg_t.data_ptr(), n,
+                                  spec.element_size, spec.bit_reorder, long_codes, weight_offset, cols,
+                                  x_t.data_ptr(), batch, partials.data_ptr(), len(tiles), stream)
+        _native.matvec_reduce(index_t.data_ptr(), entries_t.data_ptr(), rows, partials.data_ptr(), batch,
+                              spec.element_size, spec.bit_reorder, None if bias_t is None else bias_t.data_ptr(),
+                              y.data_ptr(), stream)
+        torch.cuda.synchronize(device)
+        outs.append(y.cpu())
+    return outs
+
+
+def check_product(y, w, x, bias, dtype):
+    w64, x64 = w.double().numpy(), x.double().numpy()
+    ref = x64 @ w64.T + (0 if bias is None else bias.double().numpy())
+    scale = np.abs(x64) @ np.abs(w64).T
+    delta = w.shape[1] * 2.0 ** -24 * scale + 1e-30
+    tol = HALF_ULP[dtype] * (np.abs(ref) + delta) + delta
+    got = y.double().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert (err <= tol).all(), f"max error {err.max():.3g}, worst ratio {(err / tol).max():.3g}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("case", ["huff0", "nzm1"])
+def test_matvec_matches_the_exact_product(case, dtype, batch):
+    w, enc, offset = encoded_case(case, dtype)
+    base, descs, tiles = enc.host_image()
+    rows, cols = w.shape
+    g = torch.Generator().manual_seed(batch)
+    x = torch.randn(batch, cols, generator=g).to(dtype)
+    bias = (torch.randn(rows, generator=g) * 0.1).to(dtype) if batch == 3 else None
+    first, second = run_matvec(base, descs, tiles, dtype, offset, rows, cols, x, bias)
+    assert torch.equal(first.view(torch.uint8), second.view(torch.uint8)), "repeated calls differ"
+    check_product(first, w, x, bias, dtype)
+
+
+@pytest.mark.gpu
+def test_matvec_long_codes():
+    w, enc, offset = encoded_case("long", torch.bfloat16)
+    base, descs, tiles = enc.host_image()
+    assert (descs["kind"] == _native.KIND_LONG).any()
+    rows, cols = w.shape
+    x = torch.randn(2, cols, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    first, second = run_matvec(base, descs, tiles, torch.bfloat16, offset, rows, cols, x)
+    assert torch.equal(first.view(torch.uint8), second.view(torch.uint8))
+    check_product(first, w, x, None, torch.bfloat16)
