@@ -226,7 +226,7 @@ def model_benchmark(args):
     log(f"setup: {len(setup.codebooks)} codebooks in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     exported = export_model_for_gpu(model, setup)
-    runtime = NeuralZipRuntime.attach(model, exported, device=device)
+    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=args.matvec)
     log(f"export + attach: {len(exported.groups)} fragments, {len(exported.block_order)} blocks "
         f"in {time.perf_counter() - t0:.1f}s")
     with torch.no_grad():
@@ -246,6 +246,30 @@ def model_benchmark(args):
     pass_ms = a.elapsed_time(b) / passes
     decoded_bytes = sum(g.encoded.raw_bytes for g in exported.groups)
     log(f"full decode pass: {pass_ms:.3f} ms, {decoded_bytes / pass_ms / 1e6:.0f} GB/s decoded")
+    matvec = {}
+    if runtime._matvec:
+        # one fused product (one activation row) per compressed Linear, back to back
+        plans = list(runtime._matvec.values())
+        xs = [torch.randn(1, p.cols, device=device).to(p.dtype) for p in plans]
+
+        def matvec_pass():
+            for plan, x in zip(plans, xs):
+                runtime._decoder.matvec(plan, x, None, runtime._partials, stream)
+        matvec_pass()
+        a.record(stream)
+        for _ in range(passes):
+            matvec_pass()
+        b.record(stream)
+        torch.cuda.synchronize(device)
+        mv_ms = a.elapsed_time(b) / passes
+        weights = sum(p.rows * p.cols * torch.empty((), dtype=p.dtype).element_size() for p in plans)
+        reads = sum(p.algorithmic_bytes for p in plans)
+        log(f"full fused matvec pass: {mv_ms:.3f} ms over {len(plans)} weights, {reads / mv_ms / 1e6:.0f} GB/s "
+            f"read, {weights / mv_ms / 1e6:.0f} GB/s of {args.dtype} weights")
+        matvec = {"fused_matvec_tokens": args.matvec, "full_matvec_pass_ms": round(mv_ms, 3),
+                  "full_matvec_pass_read_gbps": round(reads / mv_ms / 1e6, 1),
+                  "full_matvec_pass_weight_gbps": round(weights / mv_ms / 1e6, 1),
+                  "fused_blocks": len(runtime._matvec_blocks)}
     torch.cuda.empty_cache()
     torch.cuda.reset_peak_memory_stats(device)
     nz_s, nz_out = time_generate(model, ids, new_tokens)
@@ -277,14 +301,18 @@ def model_benchmark(args):
                    "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
-                   "prefetch": runtime.prefetch},
+                   "prefetch": runtime.prefetch, **matvec},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
         "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
+        # generated tokens before the first position where any sequence differs
+        "matching_token_prefix": int((nz_out[:, prompt:].cpu() == base_out[:, prompt:].cpu()).all(0).int()
+                                     .cumprod(0).sum()),
     }
     print(json.dumps(line), flush=True)
-    return 0 if line["logits_bitwise_equal"] and line["tokens_identical"] else 1
+    # fused products are not bit-identical to the GEMM, so generated tokens may differ there
+    return 0 if line["logits_bitwise_equal"] and (line["tokens_identical"] or args.matvec) else 1
 
 
 def main():
@@ -303,6 +331,9 @@ def main():
     parser.add_argument("--dtype", choices=sorted(WEIGHT_DTYPES), default="bf16",
                         help="weight dtype of the model benchmark")
     parser.add_argument("--batch", type=int, default=1)
+    parser.add_argument("--matvec", type=int, default=0,
+                        help="model benchmark: fused decode-matvec for blocks of at most this many token rows "
+                             "(0: always decode)")
     parser.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the model's)")
     parser.add_argument("--new-tokens", type=int, default=None, help="generated tokens (default: the model's)")
     args = parser.parse_args()

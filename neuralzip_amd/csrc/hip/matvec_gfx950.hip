@@ -362,8 +362,17 @@ void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint3
                       : word_to_float<ES, REORDER>(ES == 2 ? reinterpret_cast<const uint16_t*>(bias)[n]
                                                            : reinterpret_cast<const uint32_t*>(bias)[n]);
     for (uint32_t b = 0; b < batch; ++b) {
+        // four entries' loads in flight at a time; the additions keep entry order
         float sum = 0.0f;
-        for (uint32_t e = e0; e < e1; ++e) sum += partials[entries[e] * batch + b];
+        for (uint32_t e = e0; e < e1; e += 4) {
+            float part[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                part[k] = e + k < e1 ? partials[entries[e + k] * batch + b] : 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                if (e + k < e1) sum += part[k];
+        }
         store_result<ES, REORDER>(y, b * rows + n, sum + add);
     }
 }

@@ -336,13 +336,24 @@ class NeuralZipRuntime:
     `workspaces[dtype]` holds every slot; a block's weights are views into
     its slot. With `prefetch`, consecutive blocks use different slots and
     block N+1 is decoded on `side_stream` while block N computes.
+
+    With `matvec_tokens` = T > 0 (at most _native.MATVEC_MAX_BATCH), a block
+    whose input holds at most T token rows, and whose compressed weights
+    are all nn.Linear weights the fused kernel takes, is not decoded: each
+    of its Linears computes x @ W^T + b straight from the compressed tiles
+    (fp32 accumulation, one rounding; not bit-identical to the GEMM).
+    Larger inputs decode the block as usual. No counterpart in the
+    reference, which always decodes.
     """
 
-    def __init__(self, model, exported, device, *, prefetch=True):
+    def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0):
         self.model = model
         self.export = exported
         self.device = torch.device(device)
         self.prefetch = bool(prefetch)
+        self.matvec_tokens = int(matvec_tokens)
+        if not 0 <= self.matvec_tokens <= _native.MATVEC_MAX_BATCH:
+            raise ValueError(f"matvec_tokens must be in [0, {_native.MATVEC_MAX_BATCH}].")
         self._decoder = gpu_decoder.default_decoder()
         self._hook_handles = []
         order = exported.block_order
@@ -364,11 +375,13 @@ class NeuralZipRuntime:
                 cursor += _align(block_sizes.get((dtype, slot), 0))
             self.workspaces[dtype] = torch.empty(max(cursor, 1), dtype=dtype, device=self.device)
         # the packed device store: every tensor at its slot's offset
-        tensors, by_block, frag_base = [], defaultdict(list), 0
+        tensors, by_block, frag_base, tensor_frags = [], defaultdict(list), 0, {}
         for layout, ids, offset, config, name in exported.tensors:
             slot_base = self.slot_offsets[(config.torch_dtype, self.block_slot[name])]
             tensors.append((layout, ids, slot_base + offset))
-            by_block[(name, config.torch_dtype)].extend(range(frag_base, frag_base + layout.n_fragments))
+            frags = range(frag_base, frag_base + layout.n_fragments)
+            by_block[(name, config.torch_dtype)].extend(frags)
+            tensor_frags[(name, config.torch_dtype, offset)] = frags
             frag_base += layout.n_fragments
         self.store = gpu_decoder.DeviceStore(exported.codebooks, tensors, self.device)
         self._prepared_batches = defaultdict(list)
@@ -389,10 +402,43 @@ class NeuralZipRuntime:
         with torch.cuda.device(self.device):
             self._events = {name: (torch.cuda.Event(), torch.cuda.Event()) for name in order} if self.prefetch else {}
         self._pending = None   # (block name, event) decoded ahead on the side stream
+        self._matvec, self._matvec_blocks, self._partials = {}, frozenset(), None
+        self._fused = set()    # blocks whose current call runs the fused products
+        if self.matvec_tokens:
+            self._prepare_matvec(tensor_frags)
         torch.cuda.synchronize(self.device)
 
+    def _prepare_matvec(self, tensor_frags):
+        """Fused products of every block whose compressed weights are all
+        nn.Linear weights the fused kernel takes (rows of at least one tile)."""
+        plans, blocks = {}, []
+        for name, groups in self._groups_by_block.items():
+            bindings = dict.fromkeys((b, g.encoded.dtype) for g in groups for b in g.bindings)
+            block_plans = {}
+            for binding, spec in bindings:
+                module = self.model.get_submodule(binding.module_name)
+                if type(module) is not nn.Linear or len(binding.shape) != 2:
+                    block_plans = None
+                    break
+                rows, cols = binding.shape
+                offset = self.slot_offsets[(spec.torch_dtype, self.block_slot[name])] + binding.workspace_offset
+                frags = tensor_frags[(name, spec.torch_dtype, binding.workspace_offset)]
+                try:
+                    block_plans[binding.module_name] = self._decoder.prepare_matvec(self.store, frags, spec, offset,
+                                                                                    rows, cols)
+                except _native.NativeError:
+                    block_plans = None
+                    break
+            if block_plans:
+                plans.update(block_plans)
+                blocks.append(name)
+        self._matvec, self._matvec_blocks = plans, frozenset(blocks)
+        if plans:
+            need = max(2 * plan.n_tiles for plan in plans.values()) * self.matvec_tokens
+            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+
     @classmethod
-    def attach(cls, model, exported, *, device=None, prefetch=True):
+    def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0):
         if hasattr(model, RUNTIME_ATTRIBUTE):
             raise RuntimeError("This model already has a NeuralZip runtime.")
         if not exported.groups:
@@ -413,7 +459,7 @@ class NeuralZipRuntime:
             module._parameters.pop("weight", None)
             module.__dict__.pop("weight", None)
         model.to(device).eval()
-        runtime = cls(model, exported, device, prefetch=prefetch)
+        runtime = cls(model, exported, device, prefetch=prefetch, matvec_tokens=matvec_tokens)
         runtime._install()
         return runtime
 
@@ -429,16 +475,48 @@ class NeuralZipRuntime:
                         group.encoded.dtype.torch_dtype, name, binding)
         for name in self.export.block_order:
             handle = _decode_hook_module(self.model, name).register_forward_pre_hook(
-                partial(self._decode_block, name), prepend=True)
+                partial(self._decode_block, name), prepend=True, with_kwargs=True)
             self._hook_handles.append(handle)
+        blocks = {b.module_name: g.block_name for g in self.export.groups for b in g.bindings}
+        for module_name in self._matvec:
+            module = self.model.get_submodule(module_name)
+            module.forward = partial(self._linear_forward, blocks[module_name], module_name, module)
         setattr(self.model, RUNTIME_ATTRIBUTE, self)
 
     def _launch(self, block_name, stream):
         for prepared in self._prepared_batches[block_name]:
             self._decoder.decode_batch(prepared, stream)
 
-    def _decode_block(self, block_name, _module=None, _args=None):
+    def _token_rows(self, args, kwargs):
+        """Rows of the block's first tensor argument (its hidden states)."""
+        for value in (*args, *(kwargs or {}).values()):
+            if torch.is_tensor(value) and value.dim() >= 1 and value.shape[-1]:
+                return value.numel() // value.shape[-1]
+        return None
+
+    def _linear_forward(self, block_name, module_name, module, input):
+        if block_name in self._fused:
+            plan = self._matvec[module_name]
+            x = input.reshape(-1, plan.cols)
+            if x.shape[0] <= self.matvec_tokens:
+                y = self._decoder.matvec(plan, x, module.bias, self._partials)
+                return y.view(*input.shape[:-1], plan.rows)
+            # more rows than the block's input announced: decode it after all
+            self._fused.discard(block_name)
+            self._launch(block_name, torch.cuda.current_stream(self.device))
+        return nn.functional.linear(input, module.weight, module.bias)
+
+    def _decode_block(self, block_name, _module=None, _args=(), _kwargs=None):
         current = torch.cuda.current_stream(self.device)
+        if block_name in self._matvec_blocks:
+            rows = self._token_rows(_args, _kwargs)
+            if rows is not None and rows <= self.matvec_tokens:
+                self._fused.add(block_name)
+                pending, self._pending = self._pending, None
+                if pending is not None:   # nothing may still write a slot once decoding resumes
+                    current.wait_event(pending[1])
+                return
+            self._fused.discard(block_name)
         pending, self._pending = self._pending, None
         if pending is not None and pending[0] == block_name:
             current.wait_event(pending[1])

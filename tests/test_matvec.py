@@ -208,3 +208,91 @@ def test_matvec_long_codes():
     first, second = run_matvec(base, descs, tiles, torch.bfloat16, offset, rows, cols, x)
     assert torch.equal(first.view(torch.uint8), second.view(torch.uint8))
     check_product(first, w, x, None, torch.bfloat16)
+
+
+# ---------------------------------------------------------------- runtime
+
+class Block(torch.nn.Module):
+    def __init__(self, width, hidden):
+        super().__init__()
+        self.up = torch.nn.Linear(width, hidden, bias=True)
+        self.down = torch.nn.Linear(hidden, width, bias=False)
+
+    def forward(self, x):
+        return x + self.down(torch.nn.functional.gelu(self.up(x)))
+
+
+class BlockStack(torch.nn.Module):
+    def __init__(self, width=2048, hidden=4096, depth=3, out=3000):
+        super().__init__()
+        self.layers = torch.nn.ModuleList(Block(width, hidden) for _ in range(depth))
+        self.head = torch.nn.Linear(width, out, bias=False)
+
+    def forward(self, x):
+        for layer in self.layers:
+            x = layer(x)
+        return self.head(x)
+
+
+@pytest.mark.gpu
+def test_runtime_runs_fused_products_for_few_rows_and_decodes_otherwise():
+    import copy
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    model = BlockStack().to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(4)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(p.dtype))
+    reference = copy.deepcopy(model).cuda()
+    setup = NeuralZipSetup().build({n: p.detach() for n, p in model.named_parameters()})
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", matvec_tokens=4)
+    assert runtime._matvec_blocks == {"layers.0", "layers.1", "layers.2", "head"}
+    few = torch.randn(2, 1, 2048, generator=g).to(torch.bfloat16).cuda()
+    many = torch.randn(1, 8, 2048, generator=g).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        want_few, want_many = reference(few), reference(many)
+        outs = []
+        for _ in range(2):
+            runtime.drain()
+            torch.cuda.synchronize()
+            for workspace in runtime.workspaces.values():
+                workspace.view(torch.uint8).fill_(0xFF)       # NaN words: a read of an undecoded slot shows
+            outs.append(model(few))
+        got_many = model(many)
+        got_again = model(few)
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.equal(outs[0].view(torch.int16), got_again.view(torch.int16))
+    err = (outs[0].float() - want_few.float()).norm() / want_few.float().norm()
+    assert err < 2 ** -7, f"relative error {err:.3g}"
+    assert torch.equal(got_many.view(torch.int16), want_many.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_llama_step_after_a_decoded_prefill():
+    """Prefill (many rows) decodes and matches bit for bit; a one-token step
+    runs the fused products and stays within the rounding of bf16 layers."""
+    import copy
+    import transformers
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    config = transformers.LlamaConfig(hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,
+                                      num_attention_heads=16, num_key_value_heads=4, vocab_size=512,
+                                      max_position_embeddings=256, tie_word_embeddings=False)
+    torch.manual_seed(0)
+    model = transformers.LlamaForCausalLM(config).to(torch.bfloat16).eval()
+    reference = copy.deepcopy(model).cuda()
+    setup = NeuralZipSetup().build(model)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", matvec_tokens=1)
+    assert {"model.layers.0", "model.layers.1", "lm_head"} <= runtime._matvec_blocks
+    ids = torch.randint(0, 512, (1, 24), generator=torch.Generator().manual_seed(1)).cuda()
+    with torch.no_grad():
+        ref = reference(ids, use_cache=True)
+        got = model(ids, use_cache=True)
+        assert torch.equal(got.logits.view(torch.int16), ref.logits.view(torch.int16))
+        step = ref.logits[:, -1:].argmax(-1)
+        ref_step = reference(step, past_key_values=ref.past_key_values).logits.float()
+        got_step = model(step, past_key_values=got.past_key_values).logits.float()
+    err = (got_step - ref_step).norm() / ref_step.norm()
+    assert err < 2 ** -6, f"relative error {err:.3g}"
