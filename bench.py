@@ -246,10 +246,18 @@ def model_benchmark(args):
     pass_ms = a.elapsed_time(b) / passes
     decoded_bytes = sum(g.encoded.raw_bytes for g in exported.groups)
     log(f"full decode pass: {pass_ms:.3f} ms, {decoded_bytes / pass_ms / 1e6:.0f} GB/s decoded")
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats(device)
+    nz_s, nz_out = time_generate(model, ids, new_tokens)
+    nz_peak = torch.cuda.max_memory_allocated(device)
+    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {nz_peak / 2**30:.1f} GiB")
     matvec = {}
     if runtime._matvec:
-        # one fused product (one activation row) per compressed Linear, back to back
-        plans = list(runtime._matvec.values())
+        # one pass of fused products over every compressed Linear (one
+        # activation row), using the groups generation learned
+        grouped = {n for _, names, _ in runtime._group_plans.values() for n in names}
+        plans = [plan for plan, _, _ in runtime._group_plans.values()]
+        plans += [plan for name, plan in runtime._matvec.items() if name not in grouped]
         xs = [torch.randn(1, p.cols, device=device).to(p.dtype) for p in plans]
 
         def matvec_pass():
@@ -264,17 +272,13 @@ def model_benchmark(args):
         mv_ms = a.elapsed_time(b) / passes
         weights = sum(p.rows * p.cols * torch.empty((), dtype=p.dtype).element_size() for p in plans)
         reads = sum(p.algorithmic_bytes for p in plans)
-        log(f"full fused matvec pass: {mv_ms:.3f} ms over {len(plans)} weights, {reads / mv_ms / 1e6:.0f} GB/s "
-            f"read, {weights / mv_ms / 1e6:.0f} GB/s of {args.dtype} weights")
+        log(f"full fused matvec pass: {mv_ms:.3f} ms in {len(plans)} products ({len(runtime._group_plans)} groups), "
+            f"{reads / mv_ms / 1e6:.0f} GB/s read, {weights / mv_ms / 1e6:.0f} GB/s of {args.dtype} weights")
         matvec = {"fused_matvec_tokens": args.matvec, "full_matvec_pass_ms": round(mv_ms, 3),
                   "full_matvec_pass_read_gbps": round(reads / mv_ms / 1e6, 1),
                   "full_matvec_pass_weight_gbps": round(weights / mv_ms / 1e6, 1),
+                  "fused_products_per_pass": len(plans), "fused_groups": len(runtime._group_plans),
                   "fused_blocks": len(runtime._matvec_blocks)}
-    torch.cuda.empty_cache()
-    torch.cuda.reset_peak_memory_stats(device)
-    nz_s, nz_out = time_generate(model, ids, new_tokens)
-    nz_peak = torch.cuda.max_memory_allocated(device)
-    log(f"neuralzip: {nz_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {nz_peak / 2**30:.1f} GiB")
     steps = new_tokens - 1
     tok_s = args.batch * steps / nz_s
     base_tok_s = args.batch * steps / base_s

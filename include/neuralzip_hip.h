@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 3
+#define NZ_ABI_VERSION 4
 
 enum nz_status {
     NZ_OK = 0,
@@ -161,42 +161,56 @@ int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_t
 
 /* At most this many activation rows per fused product. */
 #define NZ_MATVEC_MAX_BATCH 4
+/* At most this many weights (sharing the activations) per fused product. */
+#define NZ_MATVEC_MAX_WEIGHTS 4
 
-/* Row index of a fused product y = x W^T + bias over one weight W (rows x
- * cols, row-major) whose elements occupy workspace indices
- * [weight_offset, weight_offset + rows * cols) of the tiles in `tiles`
- * (n_tiles of them, in launch order). Every element must be covered by
+/* One weight W (rows x cols, row-major) of a fused product y = x W^T + bias.
+ * The weights of one product share cols and the activations x; they are
+ * listed in increasing, non-overlapping workspace order, and their output
+ * rows are stacked in that order. */
+typedef struct {
+    uint64_t offset;      /* workspace element of W[0, 0] (a multiple of 16 / element_size) */
+    uint32_t rows;
+    uint32_t reserved;    /* 0 */
+    void* y;              /* nz_matvec_reduce: device output, batch x rows, weight dtype */
+    const void* bias;     /* nz_matvec_reduce: device bias (rows values) or NULL */
+} nz_matvec_weight;
+
+/* Row index of a fused product over the weights' tiles (n_tiles of them,
+ * in launch order). Every element of every weight must be covered by
  * exactly one tile and each tile may touch at most two rows (cols of at
- * least 2048 guarantees it); weight_offset and cols must be multiples of
- * 16 / element_size. Writes row_index[rows + 1] and
+ * least 2048 guarantees it). Writes row_index[total_rows + 1] and
  * entries[row_index[n] .. row_index[n + 1]) = 2 * tile + slot (slot 1 when
- * the tile started in the previous row), in element order. entries needs
- * room for 2 * n_tiles values; *n_entries receives the count.
- * No counterpart in the reference, which decodes a block into its workspace
- * before the module's own GEMM reads it (gpu/inference.py:379-509). */
-int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
-                   uint32_t rows, uint32_t cols, int element_size, uint32_t* row_index, uint32_t* entries,
-                   uint32_t capacity, uint32_t* n_entries);
+ * the tile started in the previous row) for every stacked row n, in element
+ * order. entries needs room for 2 * n_tiles values; *n_entries receives the
+ * count. No counterpart in the reference, which decodes a block into its
+ * workspace before the module's own GEMM reads it
+ * (gpu/inference.py:379-509). */
+int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                   const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
+                   uint32_t* row_index, uint32_t* entries, uint32_t capacity, uint32_t* n_entries);
 
 /* Fused decode and product, first pass: for every tile t of the segments
  * (a plan of nz_plan_work over the same tiles), the products of its
- * elements with x (device, batch x cols in the weight's dtype, 1 <= batch
+ * elements with x (device, batch x cols in the weights' dtype, 1 <= batch
  * <= NZ_MATVEC_MAX_BATCH) summed per row they touch, in
  * partials[(2 * t + slot) * batch + b] (device fp32, 2 * n_tiles * batch
- * values). One call per codebook kind (long_codes) of the weight's tiles.
+ * values). One call per codebook kind (long_codes) of the tiles.
  * Asynchronous on `stream`. No counterpart in the reference (see
  * nz_matvec_plan). */
 int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
-                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes, uint64_t weight_offset,
-                     uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream);
+                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes,
+                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
+                     uint32_t batch, float* partials, uint32_t n_tiles, void* stream);
 
-/* Second pass: y[b * rows + n] = (sum of row n's partials, in entry order)
- * + bias[n], rounded once to the weight's dtype. row_index and entries are
- * device copies of nz_matvec_plan's output; bias (device, rows values in the
- * weight's dtype) may be NULL. Asynchronous on `stream`. No counterpart in
- * the reference (see nz_matvec_plan). */
-int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows, const float* partials,
-                     uint32_t batch, int element_size, int bit_reorder, const void* bias, void* y, void* stream);
+/* Second pass: for each weight k and row n, weights[k].y[b * rows + n] =
+ * (sum of the stacked row's partials, in entry order) + bias[n], rounded
+ * once to the weights' dtype. row_index and entries are device copies of
+ * nz_matvec_plan's output. Asynchronous on `stream`. No counterpart in the
+ * reference (see nz_matvec_plan). */
+int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
+                     uint32_t n_weights, const float* partials, uint32_t batch, int element_size, int bit_reorder,
+                     void* stream);
 
 /* ---- storage format (host codecs) -------------------------------------- */
 

@@ -58,9 +58,11 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 3
+ABI_VERSION = 4
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
+# Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
+MATVEC_MAX_WEIGHTS = 4
 
 
 def lib():
@@ -89,10 +91,10 @@ def lib():
         L.nz_decode_slots.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
-        L.nz_matvec_plan.argtypes = [vp, vp, u32, u64, u32, u32, ctypes.c_int, vp, vp, u32, ctypes.POINTER(u32)]
-        L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, u64, u32, vp,
-                                       u32, vp, u32, vp]
-        L.nz_matvec_reduce.argtypes = [vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+        L.nz_matvec_plan.argtypes = [vp, vp, u32, vp, u32, u32, ctypes.c_int, vp, vp, u32, ctypes.POINTER(u32)]
+        L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, u32,
+                                       vp, u32, vp, u32, vp]
+        L.nz_matvec_reduce.argtypes = [vp, vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         _lib = L
     return _lib
 
@@ -224,27 +226,46 @@ def emulate_decode(base, descs, tiles, segments, element_size, bit_reorder, out)
                                   len(segments), int(element_size), int(bit_reorder), out.ctypes.data))
 
 
-def matvec_plan(descs, tiles, weight_offset, rows, cols, element_size):
-    """(row_index uint32[rows + 1], entries uint32[...]) of a fused product
-    over one weight whose elements the tiles cover exactly once."""
-    row_index = np.zeros(int(rows) + 1, dtype=np.uint32)
+class MatvecWeight(ctypes.Structure):
+    """nz_matvec_weight: one weight of a fused product."""
+    _fields_ = [("offset", ctypes.c_uint64), ("rows", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("y", ctypes.c_void_p), ("bias", ctypes.c_void_p)]
+
+
+def matvec_weights(entries):
+    """A ctypes array of MatvecWeight from (offset, rows[, y_ptr, bias_ptr]) tuples."""
+    array = (MatvecWeight * len(entries))()
+    for item, entry in zip(array, entries):
+        item.offset, item.rows = int(entry[0]), int(entry[1])
+        if len(entry) > 2:
+            item.y, item.bias = entry[2], entry[3]
+    return array
+
+
+def matvec_plan(descs, tiles, weights, cols, element_size):
+    """(row_index uint32[total rows + 1], entries uint32[...]) of a fused
+    product over `weights` ((workspace offset, rows) in increasing order)
+    whose elements the tiles cover exactly once."""
+    array = matvec_weights(weights)
+    row_index = np.zeros(sum(int(w[1]) for w in weights) + 1, dtype=np.uint32)
     entries = np.zeros(2 * max(len(tiles), 1), dtype=np.uint32)
     n = ctypes.c_uint32()
     tp = tiles.ctypes.data if len(tiles) else None
-    check(lib().nz_matvec_plan(descs.ctypes.data, tp, len(tiles), int(weight_offset), int(rows), int(cols),
-                               int(element_size), row_index.ctypes.data, entries.ctypes.data, len(entries),
+    check(lib().nz_matvec_plan(descs.ctypes.data, tp, len(tiles), ctypes.cast(array, ctypes.c_void_p), len(weights),
+                               int(cols), int(element_size), row_index.ctypes.data, entries.ctypes.data, len(entries),
                                ctypes.byref(n)))
     return row_index, entries[:n.value].copy()
 
 
 def matvec_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, element_size, bit_reorder, long_codes,
-                  weight_offset, cols, x_ptr, batch, partials_ptr, n_tiles, stream_ptr):
+                  weights, cols, x_ptr, batch, partials_ptr, n_tiles, stream_ptr):
+    """`weights`: a MatvecWeight array (matvec_weights)."""
     check(lib().nz_matvec_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, int(n_segments), int(element_size),
-                                 int(bit_reorder), int(long_codes), int(weight_offset), int(cols), x_ptr, int(batch),
-                                 partials_ptr, int(n_tiles), stream_ptr))
+                                 int(bit_reorder), int(long_codes), ctypes.cast(weights, ctypes.c_void_p),
+                                 len(weights), int(cols), x_ptr, int(batch), partials_ptr, int(n_tiles), stream_ptr))
 
 
-def matvec_reduce(row_index_ptr, entries_ptr, rows, partials_ptr, batch, element_size, bit_reorder, bias_ptr, y_ptr,
-                  stream_ptr):
-    check(lib().nz_matvec_reduce(row_index_ptr, entries_ptr, int(rows), partials_ptr, int(batch), int(element_size),
-                                 int(bit_reorder), bias_ptr, y_ptr, stream_ptr))
+def matvec_reduce(row_index_ptr, entries_ptr, weights, partials_ptr, batch, element_size, bit_reorder, stream_ptr):
+    """`weights`: a MatvecWeight array whose y (and bias) pointers are set."""
+    check(lib().nz_matvec_reduce(row_index_ptr, entries_ptr, ctypes.cast(weights, ctypes.c_void_p), len(weights),
+                                 partials_ptr, int(batch), int(element_size), int(bit_reorder), stream_ptr))

@@ -42,12 +42,12 @@ extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_c
                                    size_t message_size);
 extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
-                                    uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch,
-                                    float* partials, uint32_t n_tiles, void* stream, char* message,
+                                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
+                                    uint32_t batch, float* partials, uint32_t n_tiles, void* stream, char* message,
                                     size_t message_size);
-extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows,
-                                    const float* partials, uint32_t batch, int element_size, int bit_reorder,
-                                    const void* bias, void* y, void* stream, char* message, size_t message_size);
+extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
+                                    uint32_t n_weights, const float* partials, uint32_t batch, int element_size,
+                                    int bit_reorder, void* stream, char* message, size_t message_size);
 
 extern "C" {
 
@@ -213,15 +213,15 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
     return 0;
 }
 
-int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
-                   uint32_t rows, uint32_t cols, int element_size, uint32_t* row_index, uint32_t* entries,
-                   uint32_t capacity, uint32_t* n_entries) {
+int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                   const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
+                   uint32_t* row_index, uint32_t* entries, uint32_t capacity, uint32_t* n_entries) {
     return guarded([&] {
-        if (!frags || (!tiles && n_tiles) || !row_index || !entries || !n_entries)
+        if (!frags || (!tiles && n_tiles) || !weights || !row_index || !entries || !n_entries)
             nz::fail(nz::kInvalidArgument, "Null matvec plan argument.");
         if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
         std::vector<uint32_t> index, list;
-        nz::plan_matvec(frags, tiles, n_tiles, weight_offset, rows, cols, static_cast<unsigned>(element_size), index,
+        nz::plan_matvec(frags, tiles, n_tiles, weights, n_weights, cols, static_cast<unsigned>(element_size), index,
                         list);
         if (list.size() > capacity) nz::fail(nz::kInvalidArgument, "Entry buffer is too small.");
         std::copy(index.begin(), index.end(), row_index);
@@ -231,28 +231,38 @@ int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_t
 }
 
 int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
-                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes, uint64_t weight_offset,
-                     uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream) {
-    if (n_segments && (!base || !frags || !tiles || !segments || !x || !partials))
+                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes,
+                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
+                     uint32_t batch, float* partials, uint32_t n_tiles, void* stream) {
+    if (n_segments && (!base || !frags || !tiles || !segments || !x || !partials || !weights))
         return set_error(nz::kInvalidArgument, "Null matvec argument.");
-    if (cols == 0 || static_cast<uint64_t>(batch) * cols * static_cast<uint64_t>(element_size) > 0xFFFFFFFFull)
-        return set_error(nz::kInvalidArgument, "Activation rows exceed the addressable range.");
+    const int rc0 = guarded([&] {
+        if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
+        nz::check_matvec_group(weights, n_weights, cols, static_cast<unsigned>(element_size));
+        if (static_cast<uint64_t>(batch) * cols * static_cast<uint64_t>(element_size) > 0xFFFFFFFFull)
+            nz::fail(nz::kInvalidArgument, "Activation rows exceed the addressable range.");
+    });
+    if (rc0) return rc0;
     char message[256] = {0};
     const int rc = nz_hip_matvec_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
-                                        long_codes, weight_offset, cols, x, batch, partials, n_tiles, stream, message,
-                                        sizeof message);
+                                        long_codes, weights, n_weights, cols, x, batch, partials, n_tiles, stream,
+                                        message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }
 
-int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows, const float* partials,
-                     uint32_t batch, int element_size, int bit_reorder, const void* bias, void* y, void* stream) {
-    if (rows && (!row_index || !entries || !partials || !y))
-        return set_error(nz::kInvalidArgument, "Null matvec reduce argument.");
+int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
+                     uint32_t n_weights, const float* partials, uint32_t batch, int element_size, int bit_reorder,
+                     void* stream) {
+    if (!row_index || !entries || !partials || !weights) return set_error(nz::kInvalidArgument, "Null matvec reduce argument.");
+    if (n_weights == 0 || n_weights > NZ_MATVEC_MAX_WEIGHTS)
+        return set_error(nz::kInvalidArgument, "A fused product takes 1 to 4 weights.");
     if (batch > NZ_MATVEC_MAX_BATCH) return set_error(nz::kInvalidArgument, "matvec batch exceeds the maximum.");
+    for (uint32_t k = 0; k < n_weights; ++k)
+        if (!weights[k].y) return set_error(nz::kInvalidArgument, "Null matvec output.");
     char message[256] = {0};
-    const int rc = nz_hip_matvec_reduce(row_index, entries, rows, partials, batch, element_size, bit_reorder, bias,
-                                        y, stream, message, sizeof message);
+    const int rc = nz_hip_matvec_reduce(row_index, entries, weights, n_weights, partials, batch, element_size,
+                                        bit_reorder, stream, message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }

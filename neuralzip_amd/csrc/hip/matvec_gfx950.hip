@@ -1,8 +1,9 @@
 // matvec_gfx950.hip -- fused decode and matrix-vector product for gfx950.
 //
-// y[b, n] = sum_k W[n, k] * x[b, k] + bias[n] for a row-major weight W
-// (rows x cols) stored in the layout of nz_format.h, without writing W
-// anywhere. No counterpart in the reference, which always decodes a block
+// y[b, n] = sum_k W[n, k] * x[b, k] + bias[n] for up to four row-major
+// weights W (rows x cols each) that share the activations x, stored in the
+// layout of nz_format.h, without writing W anywhere. The weights' rows are
+// stacked in workspace order; a tile finds its weight from its first element. No counterpart in the reference, which always decodes a block
 // into its workspace before the module's own GEMM reads it
 // (neuralzip/gpu/inference.py:379-509).
 //
@@ -88,6 +89,15 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// The weights of one launch, sorted by workspace offset and disjoint; their
+// output rows are stacked in this order (weight k's first row is row_base[k]).
+struct nz_matvec_group {
+    uint64_t offset[NZ_MATVEC_MAX_WEIGHTS];   // workspace element of W[0, 0]
+    uint32_t row_base[NZ_MATVEC_MAX_WEIGHTS];
+    uint32_t count;
+    uint32_t cols;
+};
+
 // Where a tile sits in the weight: staging index i holds element
 // (row0 + (i >= split), col0 + i - (i >= split ? cols : 0)).
 struct RowSpan {
@@ -96,8 +106,15 @@ struct RowSpan {
     uint32_t split;   // staging index of the next row's first element
 };
 
-__device__ __forceinline__ RowSpan row_span(uint64_t first, uint64_t weight_offset, uint32_t cols) {
-    const uint32_t rel = static_cast<uint32_t>(first - weight_offset);
+// Stacked row and column of a tile's staging index 0 (`first`, a workspace
+// element): the weight is the last one of the group starting at or before it.
+__device__ __forceinline__ RowSpan row_span(uint64_t first, const nz_matvec_group& g) {
+    uint32_t w = 0;
+#pragma unroll
+    for (uint32_t k = 1; k < NZ_MATVEC_MAX_WEIGHTS; ++k)
+        if (k < g.count && first >= g.offset[k]) w = k;
+    const uint32_t cols = g.cols;
+    const uint32_t rel = static_cast<uint32_t>(first - g.offset[w]) + g.row_base[w] * cols;
     RowSpan s;
     s.row0 = rel / cols;
     s.col0 = rel - s.row0 * cols;
@@ -196,8 +213,9 @@ __device__ __forceinline__ void multiply_tile(const TileInfo& ti, const Fetch<ES
 template <int ES, bool REORDER, bool LONG, bool ESC, int BT>
 __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
                                                 const nz_work& seg, uint32_t* counter, uint32_t lane,
-                                                const uint32_t* lut, uint8_t* stage, uint64_t weight_offset,
-                                                uint32_t cols, rsrc_t x, uint32_t batch, rsrc_t partials) {
+                                                const uint32_t* lut, uint8_t* stage, const nz_matvec_group& group,
+                                                rsrc_t x, uint32_t batch, rsrc_t partials) {
+    const uint32_t cols = group.cols;
     const uint32_t n = seg.tile1 - seg.tile0;
     uint32_t t = claim(counter, lane);
     if (t >= n) return;
@@ -214,7 +232,7 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_fr
         const uint32_t after = more ? claim(counter, lane) : n;
         stage_tile<ES, LONG, ESC>(cur, fc, lut, stage, lane);
         p.clear();
-        multiply_tile<ES, REORDER, LONG, BT>(cur, fc, stage, row_span(cur.first, weight_offset, cols), x, cols, batch,
+        multiply_tile<ES, REORDER, LONG, BT>(cur, fc, stage, row_span(cur.first, group), x, cols, batch,
                                              lane, p);
         p.flush(partials, seg.tile0 + t, batch, lane);
         if (!more) break;
@@ -228,15 +246,15 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_fr
 // A raw (uncoded) tile: the exponent lane is stored as is.
 template <int ES, bool REORDER, int BT>
 __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f, const nz_tile& tile,
-                         uint64_t weight_offset, uint32_t cols, rsrc_t x, uint32_t batch, uint32_t lane,
-                         Partial<BT>& p) {
+                         const nz_matvec_group& group, rsrc_t x, uint32_t batch, uint32_t lane, Partial<BT>& p) {
+    const uint32_t cols = group.cols;
     constexpr uint32_t V = 16 / ES;
     const uint64_t A0 = f.out + tile.out0, A1 = A0 + nz_tile_elements(tile.counts);
     const uint64_t first = A0 / V * V;
     const uint32_t s0 = static_cast<uint32_t>(A0 - first), s1 = static_cast<uint32_t>(A1 - first);
     const uint32_t nv = (s1 + V - 1) / V;
     const uint64_t origin = f.out / V * V;
-    const RowSpan rs = row_span(first, weight_offset, cols);
+    const RowSpan rs = row_span(first, group);
     for (uint32_t i = lane; i < nv; i += NZ_WAVE) {
         const uint32_t g = i * V;
         const uint8_t* expo = base + f.bits + (first + g - origin);
@@ -292,9 +310,9 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
 template <int ES, bool REORDER, bool LONG, int BT>
 __global__ __launch_bounds__(kMatvecThreads) __attribute__((amdgpu_waves_per_eu(8)))
 void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
-                      const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs, uint64_t weight_offset,
-                      uint32_t cols, const uint8_t* __restrict__ xp, uint32_t batch, float* __restrict__ partials_p,
-                      uint32_t n_tiles) {
+                      const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs, nz_matvec_group group,
+                      const uint8_t* __restrict__ xp, uint32_t batch, float* __restrict__ partials_p, uint32_t n_tiles) {
+    const uint32_t cols = group.cols;
     using G = Geometry<ES>;
     __shared__ __align__(16) uint32_t s_lut[NZ_LUT_MAX_WORDS];
     __shared__ __align__(16) uint8_t s_stage[kMatvecWaves][G::kStage];
@@ -312,7 +330,7 @@ void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
         for (uint32_t t = claim(&s_claim, lane); t < n; t = claim(&s_claim, lane)) {
             const nz_tile tile = tiles[seg.tile0 + t];
             p.clear();
-            raw_tile<ES, REORDER, BT>(base, frags[tile.frag], tile, weight_offset, cols, x, batch, lane, p);
+            raw_tile<ES, REORDER, BT>(base, frags[tile.frag], tile, group, x, batch, lane, p);
             p.flush(partials, seg.tile0 + t, batch, lane);
         }
         return;
@@ -324,14 +342,14 @@ void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
     __syncthreads();
     if constexpr (LONG) {
         huffman_segment<ES, REORDER, true, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave],
-                                                     weight_offset, cols, x, batch, partials);
+                                                     group, x, batch, partials);
     } else {
         if (s_lut[0])
             huffman_segment<ES, REORDER, false, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut,
-                                                          s_stage[wave], weight_offset, cols, x, batch, partials);
+                                                          s_stage[wave], group, x, batch, partials);
         else
             huffman_segment<ES, REORDER, false, false, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut,
-                                                           s_stage[wave], weight_offset, cols, x, batch, partials);
+                                                           s_stage[wave], group, x, batch, partials);
     }
 }
 
@@ -350,17 +368,34 @@ __device__ __forceinline__ void store_result(uint8_t* y, uint32_t index, float v
     }
 }
 
+// Output rows of one fused product: weight k's rows are stacked rows
+// [row_base[k], row_base[k] + rows[k]); its results go to y[k] (batch x
+// rows[k]) with bias[k] (or none).
+struct ReduceGroup {
+    uint8_t* y[NZ_MATVEC_MAX_WEIGHTS];
+    const uint8_t* bias[NZ_MATVEC_MAX_WEIGHTS];
+    uint32_t rows[NZ_MATVEC_MAX_WEIGHTS];
+    uint32_t row_base[NZ_MATVEC_MAX_WEIGHTS];
+    uint32_t count;
+    uint32_t total_rows;
+};
+
 template <int ES, bool REORDER>
 __global__ __launch_bounds__(kReduceThreads)
 void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint32_t* __restrict__ entries,
-                             uint32_t rows, const float* __restrict__ partials, uint32_t batch,
-                             const uint8_t* __restrict__ bias, uint8_t* __restrict__ y) {
+                             const float* __restrict__ partials, uint32_t batch, ReduceGroup g) {
     const uint32_t n = blockIdx.x * kReduceThreads + threadIdx.x;
-    if (n >= rows) return;
-    const uint32_t e0 = row_index[n], e1 = row_index[n + 1];
+    if (n >= g.total_rows) return;
+    uint32_t w = 0;
+#pragma unroll
+    for (uint32_t k = 1; k < NZ_MATVEC_MAX_WEIGHTS; ++k)
+        if (k < g.count && n >= g.row_base[k]) w = k;
+    const uint32_t local = n - g.row_base[w];
+    const uint8_t* bias = g.bias[w];
     const float add = bias == nullptr ? 0.0f
-                      : word_to_float<ES, REORDER>(ES == 2 ? reinterpret_cast<const uint16_t*>(bias)[n]
-                                                           : reinterpret_cast<const uint32_t*>(bias)[n]);
+                      : word_to_float<ES, REORDER>(ES == 2 ? reinterpret_cast<const uint16_t*>(bias)[local]
+                                                           : reinterpret_cast<const uint32_t*>(bias)[local]);
+    const uint32_t e0 = row_index[n], e1 = row_index[n + 1];
     for (uint32_t b = 0; b < batch; ++b) {
         // four entries' loads in flight at a time; the additions keep entry order
         float sum = 0.0f;
@@ -373,27 +408,26 @@ void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint3
             for (uint32_t k = 0; k < 4; ++k)
                 if (e + k < e1) sum += part[k];
         }
-        store_result<ES, REORDER>(y, b * rows + n, sum + add);
+        store_result<ES, REORDER>(g.y[w], b * g.rows[w] + local, sum + add);
     }
 }
 
 template <int ES, bool REORDER, bool LONG, int BT>
 hipError_t launch_matvec(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
-                         uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch, float* partials,
+                         const nz_matvec_group& group, const void* x, uint32_t batch, float* partials,
                          uint32_t n_tiles, hipStream_t stream) {
     hipLaunchKernelGGL((nz_matvec_kernel<ES, REORDER, LONG, BT>), dim3(n_segs), dim3(kMatvecThreads), 0, stream,
                        static_cast<const uint8_t*>(base), static_cast<const nz_frag_desc*>(frags),
-                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs), weight_offset, cols,
+                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs), group,
                        static_cast<const uint8_t*>(x), batch, partials, n_tiles);
     return hipGetLastError();
 }
 
 template <int ES, bool REORDER, bool LONG>
 hipError_t launch_batch(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
-                        uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch, float* partials,
+                        const nz_matvec_group& group, const void* x, uint32_t batch, float* partials,
                         uint32_t n_tiles, hipStream_t stream) {
-#define NZ_MATVEC(BT) \
-    launch_matvec<ES, REORDER, LONG, BT>(base, frags, tiles, segs, n_segs, weight_offset, cols, x, batch, partials, n_tiles, stream)
+#define NZ_MATVEC(BT) launch_matvec<ES, REORDER, LONG, BT>(base, frags, tiles, segs, n_segs, group, x, batch, partials, n_tiles, stream)
     if (batch <= 1) return NZ_MATVEC(1);
     if (batch <= 2) return NZ_MATVEC(2);
     return NZ_MATVEC(4);
@@ -409,14 +443,27 @@ bool layout_ok(int element_size, int bit_reorder, char* message, size_t message_
 
 }  // namespace
 
-// Partial sums of one launch (one codebook kind) of a weight's tiles: writes
+// Partial sums of one launch (one codebook kind) of a group's tiles: writes
 // partials[(2 * t + slot) * batch + b] for every tile t the segments cover.
+// The caller has validated the group (sorted, disjoint weights).
 extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
-                                    uint64_t weight_offset, uint32_t cols, const void* x, uint32_t batch,
-                                    float* partials, uint32_t n_tiles, void* stream, char* message,
+                                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
+                                    uint32_t batch, float* partials, uint32_t n_tiles, void* stream, char* message,
                                     size_t message_size) {
     if (n_segs == 0) return 0;
+    if (n_weights == 0 || n_weights > NZ_MATVEC_MAX_WEIGHTS) {
+        snprintf(message, message_size, "matvec groups hold 1 to %d weights (got %u).", NZ_MATVEC_MAX_WEIGHTS,
+                 n_weights);
+        return -1;
+    }
+    nz_matvec_group group = {};
+    group.count = n_weights;
+    group.cols = cols;
+    for (uint32_t k = 0, base_row = 0; k < n_weights; base_row += weights[k].rows, ++k) {
+        group.offset[k] = weights[k].offset;
+        group.row_base[k] = base_row;
+    }
     if (!layout_ok(element_size, bit_reorder, message, message_size)) return -1;
     if (batch == 0 || batch > NZ_MATVEC_MAX_BATCH) {
         snprintf(message, message_size, "matvec batch must be in [1, %d] (got %u).", NZ_MATVEC_MAX_BATCH, batch);
@@ -424,7 +471,7 @@ extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const v
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t rc;
-#define NZ_BATCH(E, R, L) launch_batch<E, R, L>(base, frags, tiles, segs, n_segs, weight_offset, cols, x, batch, partials, n_tiles, st)
+#define NZ_BATCH(E, R, L) launch_batch<E, R, L>(base, frags, tiles, segs, n_segs, group, x, batch, partials, n_tiles, st)
     if (element_size == 2 && bit_reorder)
         rc = long_codes ? NZ_BATCH(2, true, true) : NZ_BATCH(2, true, false);
     else if (element_size == 2)
@@ -439,25 +486,34 @@ extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const v
     return 0;
 }
 
-// y[b * rows + n] = sum of row n's partial sums (+ bias[n]), in the weight's dtype.
-extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, uint32_t rows,
-                                    const float* partials, uint32_t batch, int element_size, int bit_reorder,
-                                    const void* bias, void* y, void* stream, char* message, size_t message_size) {
-    if (rows == 0 || batch == 0) return 0;
+// Row n of the stacked output: sum of its partial sums (+ its weight's bias),
+// rounded to the weight's dtype, into that weight's output.
+extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
+                                    uint32_t n_weights, const float* partials, uint32_t batch, int element_size,
+                                    int bit_reorder, void* stream, char* message, size_t message_size) {
+    if (n_weights == 0 || batch == 0) return 0;
     if (!layout_ok(element_size, bit_reorder, message, message_size)) return -1;
+    ReduceGroup g = {};
+    g.count = n_weights;
+    for (uint32_t k = 0; k < n_weights; ++k) {
+        g.y[k] = static_cast<uint8_t*>(weights[k].y);
+        g.bias[k] = static_cast<const uint8_t*>(weights[k].bias);
+        g.rows[k] = weights[k].rows;
+        g.row_base[k] = g.total_rows;
+        g.total_rows += weights[k].rows;
+    }
+    if (g.total_rows == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid((rows + kReduceThreads - 1) / kReduceThreads);
-    const uint8_t* b = static_cast<const uint8_t*>(bias);
-    uint8_t* out = static_cast<uint8_t*>(y);
+    const dim3 grid((g.total_rows + kReduceThreads - 1) / kReduceThreads);
     if (element_size == 2 && bit_reorder)
         hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, true>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
-                           rows, partials, batch, b, out);
+                           partials, batch, g);
     else if (element_size == 2)
         hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, false>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
-                           rows, partials, batch, b, out);
+                           partials, batch, g);
     else
         hipLaunchKernelGGL((nz_matvec_reduce_kernel<4, true>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
-                           rows, partials, batch, b, out);
+                           partials, batch, g);
     const hipError_t rc = hipGetLastError();
     if (rc != hipSuccess) {
         snprintf(message, message_size, "matvec reduce launch failed: %s", hipGetErrorString(rc));

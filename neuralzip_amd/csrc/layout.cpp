@@ -210,20 +210,38 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 
 constexpr uint64_t kMinTilesPerGroup = 16;
 
-void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
-                 uint32_t rows, uint32_t cols, unsigned element_size, std::vector<uint32_t>& row_index,
-                 std::vector<uint32_t>& entries) {
+void check_matvec_group(const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, unsigned element_size) {
     if (element_size != 2 && element_size != 4) fail(kInvalidArgument, "element_size must be 2 or 4.");
+    if (!n_weights || n_weights > NZ_MATVEC_MAX_WEIGHTS) fail(kInvalidArgument, "A fused product takes 1 to 4 weights.");
     const uint32_t V = 16 / element_size;
-    if (!rows || !cols) fail(kInvalidArgument, "The weight has no elements.");
-    if (cols % V || weight_offset % V)
-        fail(kInvalidArgument, "Weight offset and row length must be multiples of 16 bytes of elements.");
-    const uint64_t numel = static_cast<uint64_t>(rows) * cols;
-    if (numel > 0xFFFFFFFFull) fail(kLayoutLimit, "The weight exceeds 2^32 elements.");
+    if (!cols || cols % V) fail(kInvalidArgument, "Row length must be a positive multiple of 16 bytes of elements.");
+    uint64_t total = 0, end = 0;
+    for (uint32_t k = 0; k < n_weights; ++k) {
+        const nz_matvec_weight& w = weights[k];
+        if (!w.rows) fail(kInvalidArgument, "A weight has no rows.");
+        if (w.offset % V) fail(kInvalidArgument, "Weight offsets must be multiples of 16 bytes of elements.");
+        if (k && w.offset < end) fail(kInvalidArgument, "Weights must be listed in increasing, disjoint order.");
+        end = w.offset + static_cast<uint64_t>(w.rows) * cols;
+        total += static_cast<uint64_t>(w.rows) * cols;
+    }
+    if (total > 0xFFFFFFFFull) fail(kLayoutLimit, "The weights exceed 2^32 elements.");
+}
+
+void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, const nz_matvec_weight* weights,
+                 uint32_t n_weights, uint32_t cols, unsigned element_size, std::vector<uint32_t>& row_index,
+                 std::vector<uint32_t>& entries) {
+    check_matvec_group(weights, n_weights, cols, element_size);
     if (static_cast<uint64_t>(n_tiles) * 2 > 0xFFFFFFFFull / (4 * NZ_MATVEC_MAX_BATCH))
         fail(kLayoutLimit, "Too many tiles for one product.");
+    uint32_t rows = 0;
+    std::vector<uint64_t> stacked(n_weights);   // first stacked element of each weight
+    for (uint32_t k = 0; k < n_weights; ++k) {
+        stacked[k] = static_cast<uint64_t>(rows) * cols;
+        rows += weights[k].rows;
+    }
+    const uint64_t numel = static_cast<uint64_t>(rows) * cols;
     struct Span {
-        uint64_t a0, a1;
+        uint64_t a0, a1;   // stacked element range
         uint32_t tile;
     };
     std::vector<Span> spans(n_tiles);
@@ -231,18 +249,21 @@ void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
         const nz_frag_desc& f = frags[tiles[t].frag];
         const uint64_t a0 = f.out + tiles[t].out0;
         const uint64_t a1 = a0 + nz_tile_elements(tiles[t].counts);
-        if (a0 < weight_offset || a1 > weight_offset + numel || a1 <= a0)
-            fail(kInvalidArgument, "A tile lies outside the weight.");
-        spans[t] = {a0 - weight_offset, a1 - weight_offset, t};
+        uint32_t w = 0;
+        for (uint32_t k = 1; k < n_weights; ++k)
+            if (a0 >= weights[k].offset) w = k;
+        const uint64_t lo = weights[w].offset, hi = lo + static_cast<uint64_t>(weights[w].rows) * cols;
+        if (a0 < lo || a1 > hi || a1 <= a0) fail(kInvalidArgument, "A tile lies outside the weights.");
+        spans[t] = {a0 - lo + stacked[w], a1 - lo + stacked[w], t};
     }
     std::sort(spans.begin(), spans.end(), [](const Span& a, const Span& b) { return a.a0 < b.a0; });
     uint64_t cursor = 0;
     for (const Span& s : spans) {
-        if (s.a0 != cursor) fail(kInvalidArgument, "The tiles do not cover the weight exactly once.");
+        if (s.a0 != cursor) fail(kInvalidArgument, "The tiles do not cover the weights exactly once.");
         if ((s.a1 - 1) / cols - s.a0 / cols > 1) fail(kLayoutLimit, "A tile spans more than two rows.");
         cursor = s.a1;
     }
-    if (cursor != numel) fail(kInvalidArgument, "The tiles do not cover the weight exactly once.");
+    if (cursor != numel) fail(kInvalidArgument, "The tiles do not cover the weights exactly once.");
     // spans are in element order, so each row's entries are appended in order
     row_index.assign(static_cast<size_t>(rows) + 1, 0);
     entries.clear();

@@ -4,6 +4,7 @@
 #include <vector>
 
 #include "codebook.hpp"
+#include "neuralzip_hip.h"
 #include "nz_format.h"
 
 namespace nz {
@@ -58,14 +59,18 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 // contiguous segments of about equal elements.
 std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots);
 
-// Row index of the fused matrix-vector product over one row-major weight
-// (rows x cols at workspace elements [weight_offset, + rows * cols)) whose
-// elements the tiles cover exactly once: row_index[rows + 1] and entries
-// (2 * tile + slot, slot 1 for a tile that started in the previous row), each
-// row's entries in element order. Fails unless every tile touches at most
-// two rows and weight_offset and cols are multiples of 16 / element_size.
-void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint64_t weight_offset,
-                 uint32_t rows, uint32_t cols, unsigned element_size, std::vector<uint32_t>& row_index,
+// Checks a fused product's weight list: 1..NZ_MATVEC_MAX_WEIGHTS weights,
+// aligned offsets in increasing disjoint order, cols a multiple of 16 bytes
+// of elements, under 2^32 stacked elements.
+void check_matvec_group(const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, unsigned element_size);
+
+// Row index of the fused matrix-vector product over the weights (rows
+// stacked in list order) whose elements the tiles cover exactly once:
+// row_index[total rows + 1] and entries (2 * tile + slot, slot 1 for a
+// tile that started in the previous row), each row's entries in element
+// order. Fails unless every tile touches at most two rows.
+void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, const nz_matvec_weight* weights,
+                 uint32_t n_weights, uint32_t cols, unsigned element_size, std::vector<uint32_t>& row_index,
                  std::vector<uint32_t>& entries);
 
 // CPU emulation of the decode kernel over a packed buffer; writes words

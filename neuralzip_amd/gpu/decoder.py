@@ -150,31 +150,34 @@ class HIPDecoder:
                 cache[(device, key)] = _native.decode_slots(*key)
         return cache[(device, key)]
 
-    def prepare_matvec(self, store, fragment_indices, dtype, weight_offset, rows, cols, slots=SLOTS):
-        """Fused product over the weight (rows x cols, row-major, at workspace
-        element `weight_offset`) that `fragment_indices` encode. Raises
-        NativeError when the weight's tiles do not suit the fused kernel
-        (rows shorter than a tile, misaligned offsets)."""
-        fragment_indices = list(fragment_indices)
+    def prepare_matvec(self, store, members, dtype, cols, slots=SLOTS):
+        """Fused product over `members`, (fragment indices, workspace offset,
+        rows) of weights with `cols` columns that share their input. Raises
+        NativeError when the tiles do not suit the fused kernel (rows shorter
+        than a tile, misaligned offsets)."""
+        members = sorted(members, key=lambda m: int(m[1]))
+        if not members or len(members) > _native.MATVEC_MAX_WEIGHTS:
+            raise ValueError(f"A fused product takes 1 to {_native.MATVEC_MAX_WEIGHTS} weights.")
+        fragment_indices = [int(i) for frags, _, _ in members for i in frags]
         if not fragment_indices:
             raise ValueError("A fused product needs at least one fragment.")
         order = sorted(fragment_indices, key=lambda i: (int(store.descs[i]["kind"]), int(store.descs[i]["lut"]), i))
         tiles = np.concatenate([store.fragment_tiles(i) for i in order])
-        row_index, entries = _native.matvec_plan(store.descs, tiles, weight_offset, rows, cols, dtype.element_size)
+        weights = tuple((int(offset), int(rows)) for _, offset, rows in members)
+        row_index, entries = _native.matvec_plan(store.descs, tiles, weights, cols, dtype.element_size)
         device = store.device
-        longs = [bool(store.descs[i]["kind"] == KIND_LONG) for i in fragment_indices]
-        key = (dtype.element_size, bool(dtype.bit_reorder), any(longs))
+        key = (dtype.element_size, bool(dtype.bit_reorder),
+               any(store.descs[i]["kind"] == KIND_LONG for i in fragment_indices))
         if slots is None:
             slots = self.slots(device, key)
         segments = _native.plan_work(store.descs, tiles, slots)
         # one launch per kernel variant: segments of long-code fragments apart
         is_long = segments["kind"] == KIND_LONG
-        groups = [segments[~is_long], segments[is_long]]
         tensors = [torch.from_numpy(tiles.view(np.uint8).copy()).to(device),
                    torch.from_numpy(row_index.view(np.uint8).copy()).to(device),
                    torch.from_numpy(entries.view(np.uint8).copy()).to(device)]
         launches = []
-        for long_codes, group in enumerate(groups):
+        for long_codes, group in enumerate((segments[~is_long], segments[is_long])):
             if len(group):
                 t = torch.from_numpy(group.view(np.uint8).copy()).to(device)
                 tensors.append(t)
@@ -185,22 +188,29 @@ class HIPDecoder:
         bits = np.where(raw, numel, (descs["bit_length"].astype(np.int64) + 7) // 8)
         windows = np.where(raw, 0, (descs["bit_length"].astype(np.int64) + WINDOW_BITS - 1) // WINDOW_BITS)
         reads = int(bits.sum() + 2 * windows.sum() + (numel * (dtype.element_size - 1)).sum())
-        return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, int(rows), int(cols), len(tiles),
-                              int(weight_offset), store, tuple(launches), reads)
+        return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, weights, int(cols), len(tiles),
+                              store, tuple(launches), _native.matvec_weights(weights), reads)
 
-    def matvec(self, prepared, x, bias=None, partials=None, stream=None):
-        """y = x @ W^T (+ bias) for x of shape (batch, cols), batch <=
-        MATVEC_MAX_BATCH, in the weight's dtype; `partials` (fp32, at least
-        2 * n_tiles * batch values) is the scratch of the first pass. Returns
-        a new (batch, rows) tensor; ordered on `stream` (default: current)."""
+    def matvec(self, prepared, x, biases=None, partials=None, stream=None):
+        """x @ W^T (+ bias) for each weight of the product: x is (batch, cols),
+        batch <= MATVEC_MAX_BATCH, in the weights' dtype; `biases` is None or
+        one bias (or None) per weight; `partials` (fp32, at least
+        2 * n_tiles * batch values) is the first pass's scratch. Returns a
+        tuple of new (batch, rows) tensors, ordered on `stream` (default:
+        current)."""
         batch = x.shape[0]
         if x.dim() != 2 or x.shape[1] != prepared.cols or not 1 <= batch <= _native.MATVEC_MAX_BATCH:
             raise ValueError(f"matvec input must be (1..{_native.MATVEC_MAX_BATCH}, {prepared.cols}); "
                              f"got {tuple(x.shape)}.")
         if x.dtype != prepared.dtype or x.device != prepared.device:
-            raise ValueError("matvec input must match the weight's dtype and device.")
-        if bias is not None and (bias.dtype != prepared.dtype or bias.numel() != prepared.rows):
-            raise ValueError("matvec bias must match the weight's dtype and rows.")
+            raise ValueError("matvec input must match the weights' dtype and device.")
+        biases = tuple(biases) if biases is not None else (None,) * len(prepared.weights)
+        if len(biases) != len(prepared.weights):
+            raise ValueError("matvec needs one bias (or None) per weight.")
+        for bias, (_, rows) in zip(biases, prepared.weights):
+            if bias is not None and (bias.dtype != prepared.dtype or bias.numel() != rows or not bias.is_contiguous()
+                                     or bias.device != prepared.device):
+                raise ValueError("matvec bias must be contiguous and match the weight's dtype, rows and device.")
         x = x.contiguous()
         need = 2 * prepared.n_tiles * batch
         if partials is None:
@@ -209,18 +219,20 @@ class HIPDecoder:
             raise ValueError("matvec partials buffer is too small.")
         if stream is None:
             stream = torch.cuda.current_stream(prepared.device)
-        y = torch.empty((batch, prepared.rows), dtype=prepared.dtype, device=prepared.device)
+        ys = tuple(torch.empty((batch, rows), dtype=prepared.dtype, device=prepared.device)
+                   for _, rows in prepared.weights)
         tiles_t, row_index_t, entries_t = prepared.device_tensors[:3]
         es, reorder = prepared.layout
         for segments_ptr, n_segments, long_codes in prepared.launches:
             _native.matvec_launch(prepared.store.buffer.data_ptr(), prepared.store.frags.data_ptr(),
                                   tiles_t.data_ptr(), segments_ptr, n_segments, es, int(reorder), long_codes,
-                                  prepared.weight_offset, prepared.cols, x.data_ptr(), batch, partials.data_ptr(),
+                                  prepared.launch_weights, prepared.cols, x.data_ptr(), batch, partials.data_ptr(),
                                   prepared.n_tiles, stream.cuda_stream)
-        _native.matvec_reduce(row_index_t.data_ptr(), entries_t.data_ptr(), prepared.rows, partials.data_ptr(), batch,
-                              es, int(reorder), None if bias is None else bias.contiguous().data_ptr(), y.data_ptr(),
-                              stream.cuda_stream)
-        return y
+        outputs = _native.matvec_weights([(offset, rows, y.data_ptr(), None if b is None else b.data_ptr())
+                                          for (offset, rows), y, b in zip(prepared.weights, ys, biases)])
+        _native.matvec_reduce(row_index_t.data_ptr(), entries_t.data_ptr(), outputs, partials.data_ptr(), batch, es,
+                              int(reorder), stream.cuda_stream)
+        return ys
 
     def decode_batch(self, prepared, stream=None):
         """Launches the batch on `stream` (default: the current stream); the
@@ -233,20 +245,26 @@ class HIPDecoder:
 
 @dataclass(frozen=True)
 class PreparedMatvec:
-    """One weight's fused decode and matrix-vector product: its tiles, one
-    launch per codebook kind, and the row index of the partial sums."""
-    device_tensors: tuple = field(repr=False)          # tiles, segments, row index, entries on the device
+    """A fused decode and matrix-vector product over one or more weights
+    that share their input: their tiles (one launch per codebook kind) and
+    the row index of the partial sums; output rows stacked in `weights`
+    order."""
+    device_tensors: tuple = field(repr=False)          # tiles, row index, entries, segments on the device
     device: torch.device
     layout: tuple                                      # (element_size, bit_reorder)
     dtype: torch.dtype
-    rows: int
+    weights: tuple                                     # ((workspace offset, rows), ...) in increasing order
     cols: int
     n_tiles: int
-    weight_offset: int
     store: DeviceStore = field(repr=False)
     # (segments pointer, count, long_codes) of each launch
     launches: tuple = field(repr=False, default=())
+    launch_weights: object = field(repr=False, default=None)   # MatvecWeight array of the launches
     algorithmic_bytes: int = 0
+
+    @property
+    def rows(self):
+        return sum(rows for _, rows in self.weights)
 
 
 def algorithmic_bytes(descs, dtype):

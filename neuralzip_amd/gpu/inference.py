@@ -411,10 +411,10 @@ class NeuralZipRuntime:
     def _prepare_matvec(self, tensor_frags):
         """Fused products of every block whose compressed weights are all
         nn.Linear weights the fused kernel takes (rows of at least one tile)."""
-        plans, blocks = {}, []
+        plans, members, blocks = {}, {}, []
         for name, groups in self._groups_by_block.items():
             bindings = dict.fromkeys((b, g.encoded.dtype) for g in groups for b in g.bindings)
-            block_plans = {}
+            block_plans, block_members = {}, {}
             for binding, spec in bindings:
                 module = self.model.get_submodule(binding.module_name)
                 if type(module) is not nn.Linear or len(binding.shape) != 2:
@@ -422,20 +422,75 @@ class NeuralZipRuntime:
                     break
                 rows, cols = binding.shape
                 offset = self.slot_offsets[(spec.torch_dtype, self.block_slot[name])] + binding.workspace_offset
-                frags = tensor_frags[(name, spec.torch_dtype, binding.workspace_offset)]
+                member = (tensor_frags[(name, spec.torch_dtype, binding.workspace_offset)], offset, rows)
                 try:
-                    block_plans[binding.module_name] = self._decoder.prepare_matvec(self.store, frags, spec, offset,
-                                                                                    rows, cols)
+                    block_plans[binding.module_name] = self._decoder.prepare_matvec(self.store, [member], spec, cols)
                 except _native.NativeError:
                     block_plans = None
                     break
+                block_members[binding.module_name] = (name, spec, cols, member)
             if block_plans:
                 plans.update(block_plans)
+                members.update(block_members)
                 blocks.append(name)
-        self._matvec, self._matvec_blocks = plans, frozenset(blocks)
+        self._matvec, self._matvec_members, self._matvec_blocks = plans, members, frozenset(blocks)
+        self._group_plans = {}     # first-called module -> (plan, module names in plan order, modules)
+        self._group_tried = set()
+        self._observation = None   # (input, version, [module names called with it])
+        self._outputs = {}         # module name -> (input, version, output) computed with its group
         if plans:
             need = max(2 * plan.n_tiles for plan in plans.values()) * self.matvec_tokens
             self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+
+    @staticmethod
+    def _version_of(tensor):
+        try:
+            return tensor._version
+        except RuntimeError:   # inference tensors keep no version counter
+            return None
+
+    def _learn_group(self, names):
+        """After Linears `names` were called with one input, in this order:
+        one fused product for all of them from the first one's call on."""
+        first = names[0]
+        if first in self._group_plans or first in self._group_tried:
+            return
+        self._group_tried.add(first)
+        info = [self._matvec_members[n] for n in names]
+        block, spec, cols = info[0][:3]
+        if (len(set(names)) != len(names) or len(names) > _native.MATVEC_MAX_WEIGHTS
+                or any(i[0] != block or i[1] is not spec or i[2] != cols for i in info)):
+            return
+        ordered = sorted(zip(names, info), key=lambda item: item[1][3][1])   # by workspace offset
+        try:
+            plan = self._decoder.prepare_matvec(self.store, [i[3] for _, i in ordered], spec, cols)
+        except (_native.NativeError, ValueError):
+            return
+        self._group_plans[first] = (plan, tuple(n for n, _ in ordered),
+                                    tuple(self.model.get_submodule(n) for n, _ in ordered))
+
+    def _observe(self, module_name, input, version):
+        obs = self._observation
+        if obs is not None and obs[0] is input and obs[1] == version and version is not None:
+            obs[2].append(module_name)
+            return
+        if obs is not None and len(obs[2]) > 1:
+            self._learn_group(obs[2])
+        self._observation = (input, version, [module_name])
+
+    def _fused_product(self, module_name, module, input, x, version):
+        hit = self._outputs.pop(module_name, None)
+        if hit is not None and hit[0] is input and hit[1] == version and version is not None:
+            return hit[2]
+        group = self._group_plans.get(module_name) if version is not None else None
+        if group is None:
+            return self._decoder.matvec(self._matvec[module_name], x, [module.bias], self._partials)[0]
+        plan, names, modules = group
+        ys = self._decoder.matvec(plan, x, [m.bias for m in modules], self._partials)
+        for name, y in zip(names, ys):
+            if name != module_name:
+                self._outputs[name] = (input, version, y)
+        return ys[names.index(module_name)]
 
     @classmethod
     def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0):
@@ -499,7 +554,9 @@ class NeuralZipRuntime:
             plan = self._matvec[module_name]
             x = input.reshape(-1, plan.cols)
             if x.shape[0] <= self.matvec_tokens:
-                y = self._decoder.matvec(plan, x, module.bias, self._partials)
+                version = self._version_of(input)
+                y = self._fused_product(module_name, module, input, x, version)
+                self._observe(module_name, input, version)
                 return y.view(*input.shape[:-1], plan.rows)
             # more rows than the block's input announced: decode it after all
             self._fused.discard(block_name)

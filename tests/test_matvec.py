@@ -102,7 +102,7 @@ def test_plan_covers_each_row_in_element_order():
     _, descs, tiles = enc.host_image()
     tiles = launch_order(descs, tiles)
     rows, cols = w.shape
-    row_index, entries = _native.matvec_plan(descs, tiles, offset, rows, cols, 2)
+    row_index, entries = _native.matvec_plan(descs, tiles, [(offset, rows)], cols, 2)
     a0, a1 = tile_spans(descs, tiles, offset)
     assert row_index[0] == 0 and row_index[-1] == len(entries)
     for r in range(rows):
@@ -123,23 +123,27 @@ def test_plan_refuses_what_the_kernel_cannot_reduce():
     _, descs, tiles = enc.host_image()
     rows, cols = w.shape
     with pytest.raises(_native.NativeError, match="more than two rows"):
-        _native.matvec_plan(descs, tiles, offset, rows * 4, cols // 4, 2)     # 1024-element rows
+        _native.matvec_plan(descs, tiles, [(offset, rows * 4)], cols // 4, 2)     # 1024-element rows
     with pytest.raises(_native.NativeError, match="exactly once"):
-        _native.matvec_plan(descs, np.delete(tiles, 5), offset, rows, cols, 2)
+        _native.matvec_plan(descs, np.delete(tiles, 5), [(offset, rows)], cols, 2)
     with pytest.raises(_native.NativeError, match="multiples"):
-        _native.matvec_plan(descs, tiles, offset + 4, rows, cols, 2)
+        _native.matvec_plan(descs, tiles, [(offset + 4, rows)], cols, 2)
     with pytest.raises(_native.NativeError, match="outside"):
-        _native.matvec_plan(descs, tiles, offset, rows - 1, cols, 2)
+        _native.matvec_plan(descs, tiles, [(offset, rows - 1)], cols, 2)
+    with pytest.raises(_native.NativeError, match="increasing"):
+        _native.matvec_plan(descs, tiles, [(offset, rows), (offset + cols, 1)], cols, 2)
 
 
 # ---------------------------------------------------------------- GPU parity
 
-def run_matvec(base, descs, tiles, dtype, weight_offset, rows, cols, x, bias=None, calls=2):
-    """y of `calls` consecutive calls (partials poisoned before each)."""
+def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2):
+    """Outputs (one per weight) of `calls` consecutive calls of one fused
+    product over `weights` ((workspace offset, rows) in increasing order),
+    with the partials and outputs poisoned before each call."""
     spec = DTYPES[dtype]
     device = torch.device("cuda:0")
     tiles = launch_order(descs, tiles)
-    row_index, entries = _native.matvec_plan(descs, tiles, weight_offset, rows, cols, spec.element_size)
+    row_index, entries = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
     segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
     dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)
     base_t, frags_t, tiles_t = dev(base), dev(descs), dev(tiles)
@@ -151,23 +155,26 @@ def run_matvec(base, descs, tiles, dtype, weight_offset, rows, cols, x, bias=Non
             launches.append((dev(sel), len(sel), long_codes))
     batch = x.shape[0]
     x_t = x.contiguous().to(device)
-    bias_t = None if bias is None else bias.to(device)
+    biases = biases or [None] * len(weights)
+    bias_t = [None if b is None else b.to(device) for b in biases]
     partials = torch.empty(2 * len(tiles) * batch, dtype=torch.float32, device=device)
     stream = torch.cuda.current_stream(device).cuda_stream
-    outs = []
+    launch_weights = _native.matvec_weights(weights)
+    calls_out = []
     for _ in range(calls):
         partials.fill_(float("nan"))
-        y = torch.full((batch, rows), float("nan"), dtype=dtype, device=device)
+        ys = [torch.full((batch, rows), float("nan"), dtype=dtype, device=device) for _, rows in weights]
         for seg_t, n, long_codes in launches:
             _native.matvec_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), seg_t.data_ptr(), n,
-                                  spec.element_size, spec.bit_reorder, long_codes, weight_offset, cols,
+                                  spec.element_size, spec.bit_reorder, long_codes, launch_weights, cols,
                                   x_t.data_ptr(), batch, partials.data_ptr(), len(tiles), stream)
-        _native.matvec_reduce(index_t.data_ptr(), entries_t.data_ptr(), rows, partials.data_ptr(), batch,
-                              spec.element_size, spec.bit_reorder, None if bias_t is None else bias_t.data_ptr(),
-                              y.data_ptr(), stream)
+        outputs = _native.matvec_weights([(off, rows, y.data_ptr(), None if b is None else b.data_ptr())
+                                          for (off, rows), y, b in zip(weights, ys, bias_t)])
+        _native.matvec_reduce(index_t.data_ptr(), entries_t.data_ptr(), outputs, partials.data_ptr(), batch,
+                              spec.element_size, spec.bit_reorder, stream)
         torch.cuda.synchronize(device)
-        outs.append(y.cpu())
-    return outs
+        calls_out.append([y.cpu() for y in ys])
+    return calls_out
 
 
 def check_product(y, w, x, bias, dtype):
@@ -193,7 +200,7 @@ def test_matvec_matches_the_exact_product(case, dtype, batch):
     g = torch.Generator().manual_seed(batch)
     x = torch.randn(batch, cols, generator=g).to(dtype)
     bias = (torch.randn(rows, generator=g) * 0.1).to(dtype) if batch == 3 else None
-    first, second = run_matvec(base, descs, tiles, dtype, offset, rows, cols, x, bias)
+    (first,), (second,) = run_matvec(base, descs, tiles, dtype, [(offset, rows)], cols, x, [bias])
     assert torch.equal(first.view(torch.uint8), second.view(torch.uint8)), "repeated calls differ"
     check_product(first, w, x, bias, dtype)
 
@@ -205,21 +212,62 @@ def test_matvec_long_codes():
     assert (descs["kind"] == _native.KIND_LONG).any()
     rows, cols = w.shape
     x = torch.randn(2, cols, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
-    first, second = run_matvec(base, descs, tiles, torch.bfloat16, offset, rows, cols, x)
+    (first,), (second,) = run_matvec(base, descs, tiles, torch.bfloat16, [(offset, rows)], cols, x)
     assert torch.equal(first.view(torch.uint8), second.view(torch.uint8))
     check_product(first, w, x, None, torch.bfloat16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_product_equals_separate_products(dtype):
+    """Three weights sharing x in one launch (rows stacked in workspace order,
+    a raw chunk and two codebooks among them) give each weight the bits of
+    its own launch."""
+    cols = 4096
+    shapes = [(40, cols), (8, cols), (24, cols)]
+    ws = [random_weight(dtype, r, c, seed=10 + i) for i, (r, c) in enumerate(shapes)]
+    raws = [w.view(torch.uint8).numpy().reshape(-1).copy() for w in ws]
+    books = {0: _native.Codebook(singleton_header(raws[0], dtype)),
+             1: _native.Codebook(singleton_header(raws[2], dtype))}
+    offsets, cursor = [], 128
+    for w in ws:
+        offsets.append(cursor)
+        cursor += (w.numel() + 255) // 256 * 256 + 256
+    step = 24576
+    tensors = []
+    for i, (raw, w, off) in enumerate(zip(raws, ws, offsets)):
+        n = -(-w.numel() // step)
+        ids = [(i + j) % 2 for j in range(n)]
+        if i == 1:
+            ids[0] = -1
+        tensors.append((raw, dtype, step, ids, off))
+    base, descs, tiles = Encoded(tensors, books).host_image()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, cols, generator=g).to(dtype)
+    biases = [(torch.randn(r, generator=g) * 0.1).to(dtype) if i != 1 else None for i, (r, _) in enumerate(shapes)]
+    weights = [(off, w.shape[0]) for off, w in zip(offsets, ws)]
+    (grouped,) = run_matvec(base, descs, tiles, dtype, weights, cols, x, biases, calls=1)
+    frag_of = np.repeat(np.arange(len(ws)), [-(-w.numel() // step) for w in ws])
+    for i, (w, b) in enumerate(zip(ws, biases)):
+        own = tiles[frag_of[tiles["frag"]] == i]
+        (alone,) = run_matvec(base, descs, own, dtype, [weights[i]], cols, x, [b], calls=1)
+        assert torch.equal(grouped[i].view(torch.uint8), alone[0].view(torch.uint8)), f"weight {i}"
+        check_product(grouped[i], w, x, b, dtype)
 
 
 # ---------------------------------------------------------------- runtime
 
 class Block(torch.nn.Module):
+    """A gated MLP: gate and up read the same input (one fused group)."""
+
     def __init__(self, width, hidden):
         super().__init__()
+        self.gate = torch.nn.Linear(width, hidden, bias=False)
         self.up = torch.nn.Linear(width, hidden, bias=True)
         self.down = torch.nn.Linear(hidden, width, bias=False)
 
     def forward(self, x):
-        return x + self.down(torch.nn.functional.gelu(self.up(x)))
+        return x + self.down(torch.nn.functional.silu(self.gate(x)) * self.up(x))
 
 
 class BlockStack(torch.nn.Module):
@@ -262,6 +310,9 @@ def test_runtime_runs_fused_products_for_few_rows_and_decodes_otherwise():
         got_many = model(many)
         got_again = model(few)
     assert torch.isfinite(outs[0]).all()
+    # the first fused forward learned the gate/up groups; the second used them
+    assert {names for _, names, _ in runtime._group_plans.values()} == {
+        (f"layers.{i}.gate", f"layers.{i}.up") for i in range(3)}
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     assert torch.equal(outs[0].view(torch.int16), got_again.view(torch.int16))
     err = (outs[0].float() - want_few.float()).norm() / want_few.float().norm()
