@@ -347,3 +347,53 @@ def test_llama_step_after_a_decoded_prefill():
         got_step = model(step, past_key_values=got.past_key_values).logits.float()
     err = (got_step - ref_step).norm() / ref_step.norm()
     assert err < 2 ** -6, f"relative error {err:.3g}"
+
+
+class Widening(torch.nn.Module):
+    """A block whose input has one row per token but whose Linear sees three."""
+
+    def __init__(self, width=2048):
+        super().__init__()
+        self.proj = torch.nn.Linear(width, width, bias=False)
+
+    def forward(self, x):
+        return self.proj(torch.cat([x, 2 * x, -x], dim=-2))
+
+
+class WideningStack(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.layers = torch.nn.ModuleList([Block(2048, 2048), Widening()])
+
+    def forward(self, x):
+        return self.layers[1](self.layers[0](x))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_block_falls_back_to_decoding_when_a_linear_sees_more_rows(dtype):
+    """The hook sees one row, the Linear three (more than matvec_tokens):
+    the block is decoded on the spot and its product is the GEMM's, bit for
+    bit; the other block stays fused."""
+    import copy
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    model = WideningStack().to(dtype).eval()
+    g = torch.Generator().manual_seed(8)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(p.dtype))
+    reference = copy.deepcopy(model).cuda()
+    setup = NeuralZipSetup().build({n: p.detach() for n, p in model.named_parameters()})
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", matvec_tokens=2)
+    assert runtime._matvec_blocks == {"layers.0", "layers.1"}
+    x = torch.randn(1, 1, 2048, generator=g).to(dtype).cuda()
+    with torch.no_grad():
+        hidden_ref = reference.layers[0](x)
+        want = reference.layers[1](hidden_ref)
+        hidden = model.layers[0](x)          # fused
+        got = model.layers[1](hidden_ref)    # fused block, three rows at its Linear: decoded
+    assert "layers.1" not in runtime._fused
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    err = (hidden.float() - hidden_ref.float()).norm() / hidden_ref.float().norm()
+    assert err < 2 ** -7, f"relative error {err:.3g}"
