@@ -7,6 +7,7 @@ fragment of an export lives in one packed device buffer (DeviceStore); a
 PreparedBatch holds the tile and workgroup arrays of one launch.
 """
 from dataclasses import dataclass, field
+from functools import cached_property
 
 import numpy as np
 import torch
@@ -189,7 +190,8 @@ class HIPDecoder:
         windows = np.where(raw, 0, (descs["bit_length"].astype(np.int64) + WINDOW_BITS - 1) // WINDOW_BITS)
         reads = int(bits.sum() + 2 * windows.sum() + (numel * (dtype.element_size - 1)).sum())
         return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, weights, int(cols), len(tiles),
-                              store, tuple(launches), _native.matvec_weights(weights), reads)
+                              store, tuple(launches), _native.matvec_weights(weights), reads,
+                              _native.matvec_weights(weights))
 
     def matvec(self, prepared, x, biases=None, partials=None, stream=None):
         """x @ W^T (+ bias) for each weight of the product: x is (batch, cols),
@@ -219,8 +221,14 @@ class HIPDecoder:
             raise ValueError("matvec partials buffer is too small.")
         if stream is None:
             stream = torch.cuda.current_stream(prepared.device)
-        ys = tuple(torch.empty((batch, rows), dtype=prepared.dtype, device=prepared.device)
-                   for _, rows in prepared.weights)
+        # one allocation; weight k's (batch, rows) output is a contiguous block of it
+        out = torch.empty(batch * prepared.total_rows, dtype=prepared.dtype, device=prepared.device)
+        blocks = out.split([batch * rows for _, rows in prepared.weights])
+        reduce_weights, ys = prepared.reduce_weights, []
+        for k, ((_, rows), bias, block) in enumerate(zip(prepared.weights, biases, blocks)):
+            ys.append(block.view(batch, rows))
+            reduce_weights[k].y = block.data_ptr()
+            reduce_weights[k].bias = None if bias is None else bias.data_ptr()
         tiles_t, row_index_t, entries_t = prepared.device_tensors[:3]
         es, reorder = prepared.layout
         for segments_ptr, n_segments, long_codes in prepared.launches:
@@ -228,11 +236,9 @@ class HIPDecoder:
                                   tiles_t.data_ptr(), segments_ptr, n_segments, es, int(reorder), long_codes,
                                   prepared.launch_weights, prepared.cols, x.data_ptr(), batch, partials.data_ptr(),
                                   prepared.n_tiles, stream.cuda_stream)
-        outputs = _native.matvec_weights([(offset, rows, y.data_ptr(), None if b is None else b.data_ptr())
-                                          for (offset, rows), y, b in zip(prepared.weights, ys, biases)])
-        _native.matvec_reduce(row_index_t.data_ptr(), entries_t.data_ptr(), outputs, partials.data_ptr(), batch, es,
-                              int(reorder), stream.cuda_stream)
-        return ys
+        _native.matvec_reduce(row_index_t.data_ptr(), entries_t.data_ptr(), reduce_weights, partials.data_ptr(),
+                              batch, es, int(reorder), stream.cuda_stream)
+        return tuple(ys)
 
     def decode_batch(self, prepared, stream=None):
         """Launches the batch on `stream` (default: the current stream); the
@@ -261,9 +267,16 @@ class PreparedMatvec:
     launches: tuple = field(repr=False, default=())
     launch_weights: object = field(repr=False, default=None)   # MatvecWeight array of the launches
     algorithmic_bytes: int = 0
+    # MatvecWeight array of the reduce; each call sets its output and bias
+    # pointers (so one plan serves one call at a time)
+    reduce_weights: object = field(repr=False, default=None)
 
     @property
     def rows(self):
+        return self.total_rows
+
+    @cached_property
+    def total_rows(self):
         return sum(rows for _, rows in self.weights)
 
 
