@@ -22,7 +22,8 @@ def declared_functions():
 def test_header_declares_the_documented_entry_points():
     names = declared_functions()
     for expected in ("nz_last_error", "nz_abi_version", "nz_codebook_create", "nz_layout_encode", "nz_layout_pack",
-                     "nz_plan_work", "nz_decode_slots", "nz_decode_launch", "nz_storage_compress",
+                     "nz_plan_work", "nz_decode_slots", "nz_decode_launch", "nz_matvec_plan", "nz_matvec_launch",
+                     "nz_matvec_reduce", "nz_storage_compress",
                      "nz_storage_decompress"):
         assert expected in names
 
@@ -59,3 +60,26 @@ def test_descriptor_layouts_match_the_format_header(tmp_path):
     assert sizes == [_native.FRAG_DESC.itemsize, _native.TILE.itemsize, _native.WORK.itemsize,
                      _native.FRAG_DESC.fields["bit_length"][1], _native.FRAG_DESC.fields["numel"][1],
                      _native.TILE.fields["shape"][1], _native.WORK.fields["kind"][1]]
+
+
+def test_matvec_weight_layout_matches_the_bindings(tmp_path):
+    """nz_matvec_weight (public header, plain C) against _native.MatvecWeight."""
+    probe = tmp_path / "weight.c"
+    probe.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "neuralzip_hip.h"\n'
+        "int main(void) {\n"
+        '  printf("%zu %zu %zu %zu %zu %d %d\\n", sizeof(nz_matvec_weight), offsetof(nz_matvec_weight, rows),\n'
+        "         offsetof(nz_matvec_weight, y), offsetof(nz_matvec_weight, bias), offsetof(nz_matvec_weight, offset),\n"
+        "         NZ_MATVEC_MAX_BATCH, NZ_MATVEC_MAX_WEIGHTS);\n"
+        "  return 0;\n}\n")
+    exe = tmp_path / "weight"
+    try:
+        built = subprocess.run(["gcc", "-std=c99", "-I", str(ROOT / "include"), str(probe), "-o", str(exe)],
+                               capture_output=True, text=True)
+    except FileNotFoundError:
+        pytest.skip("no C compiler for the layout probe")
+    assert built.returncode == 0, built.stderr
+    values = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    W = _native.MatvecWeight
+    assert values == [ctypes.sizeof(W), W.rows.offset, W.y.offset, W.bias.offset, W.offset.offset,
+                      _native.MATVEC_MAX_BATCH, _native.MATVEC_MAX_WEIGHTS]
