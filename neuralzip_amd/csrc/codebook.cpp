@@ -272,9 +272,8 @@ void build_lut(Codebook& book) {
             if (pos == NZ_LUT_BITS) break;
         }
         if (count) {
-            lut[NZ_LUT_HEADER + 2 * x] = (bytes & 0xFFu) | ((bytes & 0xFF00u) << 8) |
-                                         ((32u - pos) << NZ_ENTRY_SHIFT) | (count << NZ_ENTRY_COUNT);
-            lut[NZ_LUT_HEADER + 2 * x + 1] = ((bytes >> 16) & 0xFFu) | ((bytes >> 24) << 16);
+            lut[NZ_LUT_HEADER + 2 * x] = (32u - pos) | (count << NZ_ENTRY_COUNT);
+            lut[NZ_LUT_HEADER + 2 * x + 1] = bytes;
         }
     }
     uint32_t* record = lut.data() + NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
@@ -301,8 +300,7 @@ void build_lut(Codebook& book) {
         base += static_cast<unsigned>(count);
     }
     for (size_t i = 0; i < esc.size(); ++i)
-        tokens[i] = (book.token_bytes[esc[i]] & 0xFFu) | ((book.token_bytes[esc[i]] & 0xFF00u) << 8) |
-                    (Codebook::token_width(esc[i]) << NZ_ENTRY_COUNT);
+        tokens[i] = (book.token_bytes[esc[i]] & 0xFFFFu) | (Codebook::token_width(esc[i]) << NZ_ENTRY_COUNT);
 }
 
 }  // namespace
@@ -311,9 +309,9 @@ unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* b
     const uint32_t x = static_cast<uint32_t>(window >> (64 - NZ_LUT_BITS));
     const uint32_t e = lut[NZ_LUT_HEADER + 2 * x], e1 = lut[NZ_LUT_HEADER + 2 * x + 1];
     if (e >> NZ_ENTRY_COUNT) {
-        *bytes = (e & 0xFFu) | ((e >> 8) & 0xFF00u) | ((e1 & 0xFFu) << 16) | (((e1 >> 16) & 0xFFu) << 24);
+        *bytes = e1;
         *count = e >> NZ_ENTRY_COUNT;
-        return 32u - ((e >> NZ_ENTRY_SHIFT) & 31u);
+        return 32u - (e & NZ_ENTRY_SHIFT_MASK);
     }
     const unsigned n_len = lut[0];
     const uint32_t* record = lut.data() + NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
@@ -328,7 +326,7 @@ unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* b
     const unsigned L = r[5];
     const uint32_t index = r[4] + static_cast<uint32_t>((window - first) >> (64 - L));
     const uint32_t te = record[NZ_ESC_RECORD * n_len + index];
-    *bytes = (te & 0xFFu) | ((te >> 8) & 0xFF00u);
+    *bytes = te & 0xFFFFu;
     *count = te >> NZ_ENTRY_COUNT;
     return L;
 }

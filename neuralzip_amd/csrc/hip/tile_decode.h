@@ -247,13 +247,14 @@ template <bool LONG, bool ESC>
 __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint32_t& w0, uint32_t& w1,
                                           uint32_t& w2, uint32_t& w3) {
     uint2 e = reinterpret_cast<const uint2*>(lut + NZ_LUT_HEADER)[w0 >> (32 - NZ_LUT_BITS)];
-    uint32_t s = e.x >> NZ_ENTRY_SHIFT;   // the funnel shift reads its low five bits
+    uint32_t s = e.x;   // the funnel shift reads its low five bits
     if (ESC) {
         // wave-uniform test first (one compare into a lane mask): escapes are rare
         if (__builtin_amdgcn_uicmp(e.x, 1u << NZ_ENTRY_COUNT, kIcmpUlt)) {
             if (e.x < (1u << NZ_ENTRY_COUNT)) {
                 uint32_t len;
                 e.x = escape_entry(lut, (static_cast<uint64_t>(w0) << 32) | w1, &len);
+                e.y = e.x;   // the token's bytes; the bits above them are never read back
                 if (LONG && len > 32) {
                     w0 = w1;
                     w1 = w2;
@@ -265,10 +266,10 @@ __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint
             }
         }
     }
-    p[0] = static_cast<uint8_t>(e.x);
-    p[1] = static_cast<uint8_t>(e.x >> 16);
-    p[2] = static_cast<uint8_t>(e.y);
-    p[3] = static_cast<uint8_t>(e.y >> 16);
+    p[0] = static_cast<uint8_t>(e.y);
+    p[1] = static_cast<uint8_t>(e.y >> 8);
+    p[2] = static_cast<uint8_t>(e.y >> 16);
+    p[3] = static_cast<uint8_t>(e.y >> 24);
     p += e.x >> NZ_ENTRY_COUNT;
     w0 = funnel(w0, w1, s);
     w1 = funnel(w1, w2, s);
@@ -278,7 +279,7 @@ __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint
 }
 
 // The entry's bytes b0..b3 packed into one dword, first byte lowest.
-__device__ __forceinline__ uint32_t entry_bytes(uint2 e) { return __builtin_amdgcn_perm(e.y, e.x, 0x06040200u); }
+__device__ __forceinline__ uint32_t entry_bytes(uint2 e) { return e.y; }
 
 // Decodes a tile's exponent bytes into the wavefront's staging area: staging
 // index i (from NZ_STAGE_ORIGIN) holds the byte of the element at workspace

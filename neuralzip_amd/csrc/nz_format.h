@@ -53,16 +53,15 @@
 //   then T escape token entries (one word)
 // A primary entry decodes every whole token that fits the 12-bit prefix, up
 // to four exponent bytes b0..b3:
-//   word 0: b0 | b1 << 16 | (32 - consumed bits) << 24 | byte count << 29
-//   word 1: b2 | b3 << 16
-// (consumed 1..12; byte count 1..4, 0 marks an escape). The bytes sit where
-// 8-bit stores of the low and high half-words pick them up, and the shift
-// field is what the decoder's funnel shift takes directly (it reads the low
-// five bits of its shift operand).
-// Escape token entry: b0 | b1 << 16 | byte count << 29.
+//   word 0: (32 - consumed bits) | byte count << 29
+//   word 1: b0 | b1 << 8 | b2 << 16 | b3 << 24
+// (consumed 1..12; byte count 1..4, 0 marks an escape). Word 0 is the
+// decoder's funnel-shift operand as it stands (the shift reads the low five
+// bits) and word 1 is stored as one dword.
+// Escape token entry: b0 | b1 << 8 | byte count << 29.
 #define NZ_LUT_HEADER 4
 #define NZ_ESC_RECORD 6
-#define NZ_ENTRY_SHIFT 24
+#define NZ_ENTRY_SHIFT_MASK 31u
 #define NZ_ENTRY_COUNT 29
 #define NZ_ENTRY_MAX_BYTES 4
 #define NZ_LUT_MAX_WORDS (NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES + NZ_ESC_RECORD * 56 + 512)
