@@ -239,13 +239,12 @@ __device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<E
     }
 }
 
-// One LUT step at the head of the window w0..w3: writes four bytes at *p
-// (only the entry's count of them is meaningful; the rest are overwritten
-// by the lane's next step or repaired after the loop), advances *p by the
-// count and shifts the window by the consumed bits. Returns the entry.
+// One LUT step at the head of the window w0..w3: returns the entry (byte
+// count in bits 29-31 of .x; the bytes, first lowest and zeros above them,
+// in .y) and shifts the window by the consumed bits.
 template <bool LONG, bool ESC>
-__device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint32_t& w0, uint32_t& w1,
-                                          uint32_t& w2, uint32_t& w3) {
+__device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint32_t& w0, uint32_t& w1, uint32_t& w2,
+                                          uint32_t& w3) {
     uint2 e = reinterpret_cast<const uint2*>(lut + NZ_LUT_HEADER)[w0 >> (32 - NZ_LUT_BITS)];
     uint32_t s = e.x;   // the funnel shift reads its low five bits
     if (ESC) {
@@ -254,7 +253,7 @@ __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint
             if (e.x < (1u << NZ_ENTRY_COUNT)) {
                 uint32_t len;
                 e.x = escape_entry(lut, (static_cast<uint64_t>(w0) << 32) | w1, &len);
-                e.y = e.x;   // the token's bytes; the bits above them are never read back
+                e.y = e.x & 0xFFFFu;   // one or two bytes
                 if (LONG && len > 32) {
                     w0 = w1;
                     w1 = w2;
@@ -266,20 +265,12 @@ __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint8_t*& p, uint
             }
         }
     }
-    p[0] = static_cast<uint8_t>(e.y);
-    p[1] = static_cast<uint8_t>(e.y >> 8);
-    p[2] = static_cast<uint8_t>(e.y >> 16);
-    p[3] = static_cast<uint8_t>(e.y >> 24);
-    p += e.x >> NZ_ENTRY_COUNT;
     w0 = funnel(w0, w1, s);
     w1 = funnel(w1, w2, s);
     w2 = funnel(w2, LONG ? w3 : 0u, s);
     if (LONG) w3 = funnel(w3, 0u, s);
     return e;
 }
-
-// The entry's bytes b0..b3 packed into one dword, first byte lowest.
-__device__ __forceinline__ uint32_t entry_bytes(uint2 e) { return e.y; }
 
 // Decodes a tile's exponent bytes into the wavefront's staging area: staging
 // index i (from NZ_STAGE_ORIGIN) holds the byte of the element at workspace
@@ -292,7 +283,6 @@ __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, L
     // The first window's skipped bytes land in the staging area's prefix
     // (NZ_STAGE_ORIGIN exceeds any skip, so the index stays positive).
     const uint32_t at = NZ_STAGE_ORIGIN + ti.s0 + (wave_inclusive_scan(count) - count) - ti.skip;
-    uint8_t* const first = stage + at;
     if (count) {
         uint32_t w0 = bswap32(d.w[0]), w1 = bswap32(d.w[1]), w2 = bswap32(d.w[2]), w3 = LONG ? bswap32(d.w[3]) : 0u;
         {   // restart at the gap
@@ -306,25 +296,40 @@ __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, L
                 if (LONG) w3 = funnel(w3, 0u, s);
             }
         }
-        uint8_t* p = first;
-        uint8_t* const end = first + count;
-        // The previous lane's last step may spill three bytes over this
-        // lane's first three; keep them and write them again after the loop.
-        // Every step emits at least one byte, so three steps cover them.
-        uint32_t head = entry_bytes(lut_step<LONG, ESC>(lut, p, w0, w1, w2, w3));
+        // The lane's bytes go to staging indices [at, at + count). They are
+        // gathered first-lowest in `pend` and stored as whole aligned dwords:
+        // every step stores the dword being filled, which moves on once it is
+        // complete (unaligned LDS stores cost several times more). The first
+        // and the last dword of the range may also hold a neighbour's bytes,
+        // and a neighbour's stores may leave stale bytes there. After the loop,
+        // which the wavefront leaves together, each lane stores its own bytes
+        // of those two dwords one by one, so every shared byte ends up right.
+        const uint32_t q0 = at & ~3u, q1 = (at + count - 1) & ~3u, end = at + count;
+        // fill: bits of the dword at q already taken (0, 8, 16 or 24)
+        uint32_t q = q0, fill = 8 * (at & 3u), pend = 0, lead = 0, word;
+        do {
+            const uint2 e = lut_step<LONG, ESC>(lut, w0, w1, w2, w3);
+            word = (e.y << fill) | pend;
+            *reinterpret_cast<uint32_t*>(stage + q) = word;
+            lead = q == q0 ? word : lead;
+            // the entry's bits past the dword: the top `fill` bits (none when fill is 0)
+            const uint32_t spill = __builtin_amdgcn_ubfe(e.y, 32u - fill, fill);
+            fill += e.x >> (NZ_ENTRY_COUNT - 3);   // 8 x the byte count (bits 5-28 of an entry are zero)
+            const bool full = fill >= 32;
+            pend = full ? spill : word;
+            q += full ? 4u : 0u;
+            fill &= 31u;
+        } while (q * 8 + fill < end * 8);
+        // The last dword's bytes: still pending when the loop ended on it
+        // (the final step may have filled the dword before it and spilled
+        // into it, so it was never stored), else the final store.
+        const uint32_t last = q == q1 ? pend : word;
+        const uint32_t a = at - q0, b = at + count - q1;   // own bytes: [a, 4) of q0, [0, b) of q1
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t have = static_cast<uint32_t>(p - first);
-            if (have < 3 && p < end) {
-                const uint32_t bits = 8 * have;
-                const uint32_t more = entry_bytes(lut_step<LONG, ESC>(lut, p, w0, w1, w2, w3));
-                head = (head & ((1u << bits) - 1u)) | (more << bits);
-            }
+        for (uint32_t k = 0; k < 4; ++k) {
+            if (k >= a && q0 + k < at + count) stage[q0 + k] = static_cast<uint8_t>(lead >> (8 * k));
+            if (k < b && q1 + k >= at) stage[q1 + k] = static_cast<uint8_t>(last >> (8 * k));
         }
-        while (p < end) lut_step<LONG, ESC>(lut, p, w0, w1, w2, w3);
-        first[0] = static_cast<uint8_t>(head);
-        if (count > 1) first[1] = static_cast<uint8_t>(head >> 8);
-        if (count > 2) first[2] = static_cast<uint8_t>(head >> 16);
     }
     wave_lds_sync();
 }
