@@ -82,6 +82,22 @@ def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
                       f"{decoded} bytes decoded each"}
 
 
+def host_description():
+    """The host the CPU baseline ran on: logical CPUs, the ones this process
+    may use, and the CPU model."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"os_cpu_count": os.cpu_count(), "usable_cpus": usable, "cpu_model": model}
+
+
 def copy_calibration(nbytes=1 << 30, repeats=5):
     """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE per
     dispatch scale the decode kernel's counters to bytes."""
@@ -226,7 +242,8 @@ def model_benchmark(args):
     log(f"setup: {len(setup.codebooks)} codebooks in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     exported = export_model_for_gpu(model, setup)
-    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=args.matvec)
+    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=args.matvec,
+                                      decode_slots=args.slots)
     log(f"export + attach: {len(exported.groups)} fragments, {len(exported.block_order)} blocks "
         f"in {time.perf_counter() - t0:.1f}s")
     with torch.no_grad():
@@ -305,7 +322,7 @@ def model_benchmark(args):
                    "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
-                   "prefetch": runtime.prefetch, **matvec},
+                   "prefetch": runtime.prefetch, "decode_slots": args.slots, **matvec},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
@@ -439,6 +456,10 @@ def main():
         threads = min(os.cpu_count() or 1, 16)
         baseline = cpu_baseline(tensors, setup, threads)
         log(f"cpu baseline {baseline['value']} GB/s on {threads} threads")
+        single = cpu_baseline(tensors, setup, 1, reps=3, warmups=1, budget_s=10.0)
+        log(f"cpu baseline {single['value']} GB/s on 1 thread")
+        baseline["single_thread"] = {"value": single["value"], "unit": single["unit"], "sample": single["sample"]}
+        baseline["host"] = host_description()
 
     line = {
         "metric": "decoded weight GB/s + % HBM roofline; tok/s 8B-shape bs=1 vs uncompressed bf16",

@@ -346,11 +346,12 @@ class NeuralZipRuntime:
     reference, which always decodes.
     """
 
-    def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0):
+    def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0, decode_slots=None):
         self.model = model
         self.export = exported
         self.device = torch.device(device)
         self.prefetch = bool(prefetch)
+        self.decode_slots = decode_slots   # workgroups per decode launch; None: what the device runs at once
         self.matvec_tokens = int(matvec_tokens)
         if not 0 <= self.matvec_tokens <= _native.MATVEC_MAX_BATCH:
             raise ValueError(f"matvec_tokens must be in [0, {_native.MATVEC_MAX_BATCH}].")
@@ -392,7 +393,8 @@ class NeuralZipRuntime:
             for f in frags:
                 kinds[int(self.store.descs[f]["kind"]) == KIND_LONG].append(f)
             for long_codes, members in sorted(kinds.items()):
-                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype])
+                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype],
+                                                    slots=decode_slots)
                 self._prepared_batches[name].append(batch)
                 self.algorithmic_bytes[name] = self.algorithmic_bytes.get(name, 0) + batch.algorithmic_bytes
         self._groups_by_block = defaultdict(list)
@@ -493,7 +495,7 @@ class NeuralZipRuntime:
         return ys[names.index(module_name)]
 
     @classmethod
-    def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0):
+    def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0, decode_slots=None):
         if hasattr(model, RUNTIME_ATTRIBUTE):
             raise RuntimeError("This model already has a NeuralZip runtime.")
         if not exported.groups:
@@ -514,7 +516,8 @@ class NeuralZipRuntime:
             module._parameters.pop("weight", None)
             module.__dict__.pop("weight", None)
         model.to(device).eval()
-        runtime = cls(model, exported, device, prefetch=prefetch, matvec_tokens=matvec_tokens)
+        runtime = cls(model, exported, device, prefetch=prefetch, matvec_tokens=matvec_tokens,
+                      decode_slots=decode_slots)
         runtime._install()
         return runtime
 
