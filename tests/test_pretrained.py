@@ -15,11 +15,13 @@ from neuralzip_amd.gpu import pretrained
 @pytest.fixture
 def patched():
     save, load = PreTrainedModel.save_pretrained, PreTrainedModel.__dict__["from_pretrained"]
-    state = (pretrained._Patch.save, pretrained._Patch.load, pretrained._Patch.setup, pretrained._Patch.device)
+    fields = ("save", "load", "setup", "device", "matvec_tokens")
+    state = tuple(getattr(pretrained._Patch, f) for f in fields)
     yield
     PreTrainedModel.save_pretrained = save
     PreTrainedModel.from_pretrained = load
-    pretrained._Patch.save, pretrained._Patch.load, pretrained._Patch.setup, pretrained._Patch.device = state
+    for f, value in zip(fields, state):
+        setattr(pretrained._Patch, f, value)
 
 
 def tiny_llama(tie=False, seed=0):
@@ -149,3 +151,31 @@ def test_gpu_plain_checkpoint_is_exported_and_attached(tmp_path, patched):
     with torch.no_grad():
         got = loaded(ids.cuda()).logits.float().cpu()
     assert torch.equal(got, expected)
+
+
+@pytest.mark.gpu
+def test_gpu_activation_with_fused_products(tmp_path, patched):
+    """neuralzip(..., matvec_tokens=1): from_pretrained attaches a runtime whose
+    blocks run the fused decode-matvec for one-token steps; the prefill still
+    decodes and matches bit for bit, the step stays within bf16 rounding."""
+    config = LlamaConfig(hidden_size=2048, intermediate_size=4096, num_hidden_layers=1, num_attention_heads=16,
+                         num_key_value_heads=4, vocab_size=300, max_position_embeddings=128,
+                         tie_word_embeddings=False)
+    torch.manual_seed(11)
+    model = LlamaForCausalLM(config).to(torch.bfloat16).eval()
+    model.save_pretrained(tmp_path)   # unpatched: an ordinary checkpoint
+    reference = LlamaForCausalLM.from_pretrained(tmp_path, dtype=torch.bfloat16).eval().cuda()
+    neuralzip(neuralzip.setup(model), device="cuda:0", matvec_tokens=1)
+    loaded = LlamaForCausalLM.from_pretrained(tmp_path, dtype=torch.bfloat16)
+    runtime = loaded.neuralzip_runtime
+    assert runtime.matvec_tokens == 1 and {"model.layers.0", "lm_head"} <= runtime._matvec_blocks
+    ids = torch.randint(0, 300, (1, 12), generator=torch.Generator().manual_seed(2)).cuda()
+    with torch.no_grad():
+        ref = reference(ids, use_cache=True)
+        got = loaded(ids, use_cache=True)
+        assert torch.equal(got.logits.view(torch.int16), ref.logits.view(torch.int16))
+        step = ref.logits[:, -1:].argmax(-1)
+        ref_step = reference(step, past_key_values=ref.past_key_values).logits.float()
+        got_step = loaded(step, past_key_values=got.past_key_values).logits.float()
+    err = (got_step - ref_step).norm() / ref_step.norm()
+    assert err < 2 ** -6, f"relative error {err:.3g}"
