@@ -17,6 +17,9 @@
 namespace {
 
 constexpr int kIcmpUlt = 36;   // unsigned-less-than predicate of the lane-mask compare builtin
+// s_waitcnt operand (gfx9 encoding) that waits for every outstanding LDS
+// operation: lgkmcnt 0, vmcnt 63 and expcnt 7 (no wait on those).
+constexpr int kWaitLgkm0 = 0xC07F;
 
 __device__ __forceinline__ uint32_t bswap32(uint32_t x) { return __builtin_amdgcn_perm(0u, x, 0x00010203u); }
 
@@ -276,9 +279,24 @@ __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint32_t& w0, uin
 // index i (from NZ_STAGE_ORIGIN) holds the byte of the element at workspace
 // index ti.first + i, for i in [ti.s0, ti.s1). Ends with the wavefront's LDS
 // writes visible to all of its lanes.
+//
+// The staging area is cleared first, and every write into it is an LDS
+// atomic OR of whole aligned dwords, so lanes may share a dword without any
+// ordering between them. A lane's bytes go to [at, at + count); its final
+// LUT step may emit up to three bytes past the count, and those are the next
+// window's first bytes (the bitstream is continuous: decoding on past a
+// window's last code decodes the codes that start in the next window), or,
+// after the tile's last window, bytes that no one reads. An OR therefore
+// only ever adds a byte's own value or zeros.
 template <int ES, bool LONG, bool ESC>
 __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, LONG>& d, const uint32_t* lut,
                                            uint8_t* stage, uint32_t lane) {
+    using G = Geometry<ES>;
+    constexpr uint32_t kUnits = G::kStage / 16;
+    static_assert(G::kStage % 16 == 0, "the staging area is cleared in 16-byte units");
+#pragma unroll
+    for (uint32_t u = lane; u < (kUnits + NZ_WAVE - 1) / NZ_WAVE * NZ_WAVE; u += NZ_WAVE)
+        if (u < kUnits) reinterpret_cast<uint4*>(stage)[u] = make_uint4(0u, 0u, 0u, 0u);
     const uint32_t count = lane < ti.n_win ? d.meta >> 8 : 0u;
     // The first window's skipped bytes land in the staging area's prefix
     // (NZ_STAGE_ORIGIN exceeds any skip, so the index stays positive).
@@ -296,40 +314,28 @@ __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, L
                 if (LONG) w3 = funnel(w3, 0u, s);
             }
         }
-        // The lane's bytes go to staging indices [at, at + count). They are
-        // gathered first-lowest in `pend` and stored as whole aligned dwords:
-        // every step stores the dword being filled, which moves on once it is
-        // complete (unaligned LDS stores cost several times more). The first
-        // and the last dword of the range may also hold a neighbour's bytes,
-        // and a neighbour's stores may leave stale bytes there. After the loop,
-        // which the wavefront leaves together, each lane stores its own bytes
-        // of those two dwords one by one, so every shared byte ends up right.
-        const uint32_t q0 = at & ~3u, q1 = (at + count - 1) & ~3u, end = at + count;
-        // fill: bits of the dword at q already taken (0, 8, 16 or 24)
-        uint32_t q = q0, fill = 8 * (at & 3u), pend = 0, lead = 0, word;
+        // bit: staging bit position of the next byte (8 x its index)
+        uint32_t bit = 8 * at;
+        const uint32_t stop = 8 * (at + count);
         do {
             const uint2 e = lut_step<LONG, ESC>(lut, w0, w1, w2, w3);
-            word = (e.y << fill) | pend;
-            *reinterpret_cast<uint32_t*>(stage + q) = word;
-            lead = q == q0 ? word : lead;
-            // the entry's bits past the dword: the top `fill` bits (none when fill is 0)
-            const uint32_t spill = __builtin_amdgcn_ubfe(e.y, 32u - fill, fill);
-            fill += e.x >> (NZ_ENTRY_COUNT - 3);   // 8 x the byte count (bits 5-28 of an entry are zero)
-            const bool full = fill >= 32;
-            pend = full ? spill : word;
-            q += full ? 4u : 0u;
-            fill &= 31u;
-        } while (q * 8 + fill < end * 8);
-        // The last dword's bytes: still pending when the loop ended on it
-        // (the final step may have filled the dword before it and spilled
-        // into it, so it was never stored), else the final store.
-        const uint32_t last = q == q1 ? pend : word;
-        const uint32_t a = at - q0, b = at + count - q1;   // own bytes: [a, 4) of q0, [0, b) of q1
-#pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-            if (k >= a && q0 + k < at + count) stage[q0 + k] = static_cast<uint8_t>(lead >> (8 * k));
-            if (k < b && q1 + k >= at) stage[q1 + k] = static_cast<uint8_t>(last >> (8 * k));
-        }
+            uint32_t* dst = reinterpret_cast<uint32_t*>(stage) + __builtin_amdgcn_ubfe(bit, 5u, 27u);
+            // The entry's bytes in this dword, and the ones past it. The bit
+            // field extract reads the low five bits of its offset and width,
+            // so this is ubfe(e.y, 32 - fill, fill) with fill = bit % 32: the
+            // top `fill` bits, none when fill is 0.
+            const uint32_t low = e.y << (bit & 31u);
+            const uint32_t high = __builtin_amdgcn_ubfe(e.y, 0u - bit, bit);
+            __hip_atomic_fetch_or(dst, low, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            __hip_atomic_fetch_or(dst + 1, high, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            // The ORs complete before the wavefront issues its next LDS
+            // instruction (the next LUT read). On gfx950 an LDS read issued
+            // while the same wavefront's LDS atomics were still in flight has
+            // returned staging data in place of the LUT entry, now and then;
+            // waiting here costs under 1 % of the decode time.
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            bit += e.x >> (NZ_ENTRY_COUNT - 3);   // 8 x the byte count (bits 5-28 of an entry are zero)
+        } while (bit < stop);
     }
     wave_lds_sync();
 }

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <stdexcept>
 #include <string>
 
 namespace nz {
@@ -396,14 +397,25 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
                 offset[l] = offset[l - 1] + (base[f.meta + 2 * (tile.win0 + l - 1) + 1]);
             const uint64_t s0 = A0 - A0 / V * V;
             const uint64_t origin = NZ_STAGE_ORIGIN + s0 - nz_tile_skip(tile.counts);
-            std::fill(stage.begin(), stage.end(), 0xA5);
+            // The kernel's staging rule: the area starts cleared; a lane runs
+            // LUT steps until it has emitted its window's count of bytes,
+            // and each step ORs its bytes, shifted into place, into the
+            // dword holding the first of them and the dword after it. The
+            // final step may run past the count; those bytes must be the
+            // next window's first bytes (checked below), so the ORs never
+            // change a byte that another lane owns.
+            std::fill(stage.begin(), stage.end(), 0);
+            std::vector<std::pair<uint64_t, uint8_t>> overrun;
+            auto store_or = [&](uint64_t q, uint32_t v) {
+                for (unsigned k = 0; k < 4; ++k) stage.at(q + k) |= static_cast<uint8_t>(v >> (8 * k));
+            };
             for (unsigned l = 0; l < n_win; ++l) {
                 const uint64_t w = tile.win0 + l;
                 const unsigned gap = base[f.meta + 2 * w];
+                const unsigned count = base[f.meta + 2 * w + 1];
                 const uint8_t* src = base + f.bits + 8 * w;
                 uint32_t hi = load_be32(src), mid = load_be32(src + 4), lo = load_be32(src + 8);
                 uint32_t la = longmode ? load_be32(src + 12) : 0;
-                const uint64_t end = std::min<uint64_t>(64, f.bit_length - 64 * w);
                 auto shift = [&](unsigned len) {
                     if (len >= 32) { hi = mid; mid = lo; lo = la; la = 0; len -= 32; }
                     if (len) {
@@ -415,19 +427,25 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
                     }
                 };
                 shift(gap);
-                uint64_t pos = gap;
-                uint64_t o = origin + offset[l];
-                while (pos < end) {
+                const uint64_t at = origin + offset[l], stop = at + count;
+                for (uint64_t o = at; o < stop;) {
                     const uint64_t window = (static_cast<uint64_t>(hi) << 32) | mid;
                     uint32_t bytes;
                     unsigned n;
                     const unsigned len = lut_step(lut, window, &bytes, &n);
-                    for (unsigned b = 0; b < n; ++b) stage.at(o + b) = static_cast<uint8_t>(bytes >> (8 * b));
+                    const unsigned fill = static_cast<unsigned>(8 * (o & 3));
+                    store_or(o & ~3ull, bytes << fill);
+                    store_or((o & ~3ull) + 4, fill ? bytes >> (32 - fill) : 0u);
+                    for (unsigned b = 0; b < n; ++b)
+                        if (o + b >= stop) overrun.push_back({o + b, static_cast<uint8_t>(bytes >> (8 * b))});
                     o += n;
                     shift(len);
-                    pos += len;
                 }
             }
+            const uint64_t owned = NZ_STAGE_ORIGIN + (A1 - A0 / V * V);   // bytes past it belong to no lane of the tile
+            for (const auto& [i, v] : overrun)
+                if (i < owned && stage[i] != v)
+                    throw std::runtime_error("a window's bytes past its count differ from the next window's");
             for (uint64_t g = A0; g < A1; ++g)
                 put_element(out, g, es, reorder, lane_bytes(base, f, g, es, stage[NZ_STAGE_ORIGIN + g - A0 / V * V]));
         }

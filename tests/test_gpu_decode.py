@@ -83,6 +83,21 @@ def test_segment_boundaries(max_bits, dtype):
     check_case([(raw, dtype, 1 << 20, [0], 0)], {0: book}, dtype)
 
 
+@pytest.mark.parametrize("max_bits", [33, 56])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_long_code_tiles_decode_the_same_every_time(max_bits, dtype):
+    """Tiles whose windows hold one or two long codes each: every LUT step
+    is an escape and ORs into a staging dword shared with three other lanes.
+    Without the wait for those ORs before the next LDS read, fp32 56-bit
+    decodes went wrong in most launches; eight launches in a row must all
+    match the original words and the CPU emulation."""
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(max_bits), vocab)
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
+    raw = segment_tensor(dtype, symbols)
+    check_case([(raw, dtype, 1 << 20, [0], 0)], {0: book}, dtype, repeats=4)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_raw_fragment_between_compressed_chunks_and_odd_offsets(dtype):
     spec = DTYPES[dtype]

@@ -215,3 +215,26 @@ def test_tiny_fragments_at_every_vector_phase(dtype):
         tensors.append((raw, dtype, 1 << 20, [0], offset))
         offset += n + (k % V) + 1
     emulate_case(tensors, {0: book}, dtype)
+
+
+def test_overrun_bytes_must_be_the_next_windows():
+    """The kernel's staging ORs a lane's final LUT step whole, bytes past the
+    window's count included; that is right only because those bytes are the
+    next window's first bytes. The emulator checks it for every lane; with
+    the stored counts one short, the bytes past a count are the lane's own
+    last byte, and the check must fail."""
+    spec = DTYPES[torch.bfloat16]
+    t = (torch.from_numpy(np.random.default_rng(5).standard_normal(40000).astype(np.float32)) * 0.02).bfloat16()
+    raw = t.view(torch.uint8).numpy().reshape(-1).copy()
+    book = _native.Codebook(singleton_header(raw, torch.bfloat16))
+    base, descs, tiles = Encoded([(raw, torch.bfloat16, 1 << 20, [0], 0)], {0: book}).host_image()
+    segments = _native.plan_work(descs, tiles, 512)
+    out = np.zeros(raw.size + 64, dtype=np.uint8)
+    _native.emulate_decode(base, descs, tiles, segments, spec.element_size, spec.bit_reorder, out)
+    assert np.array_equal(out[:raw.size], raw)
+    f = descs[0]
+    windows = -(-int(f["bit_length"]) // 64)
+    counts = base[int(f["meta"]) + 1:int(f["meta"]) + 2 * windows:2]   # high byte of each uint16
+    counts[counts >= 2] -= 1   # (a trailing window may hold no code)
+    with pytest.raises(Exception, match="past its count"):
+        _native.emulate_decode(base, descs, tiles, segments, spec.element_size, spec.bit_reorder, out)
