@@ -58,7 +58,7 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 4
+ABI_VERSION = 5
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
@@ -88,6 +88,7 @@ def lib():
         L.nz_layout_fragment_info.argtypes = [vp, sz, ctypes.POINTER(_FragmentInfo)]
         L.nz_layout_pack.argtypes = [vp, vp, u64, vp, u32, vp, vp]
         L.nz_plan_work.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32)]
+        L.nz_plan_work_interleaved.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32), vp]
         L.nz_decode_slots.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
@@ -206,6 +207,20 @@ def plan_work(descs, tiles, slots):
     check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), segments.ctypes.data, n.value,
                              ctypes.byref(n)))
     return segments
+
+
+def plan_work_interleaved(descs, tiles, slots):
+    """The decode launch's plan: (segments, order). Upload tiles[order]; the
+    segments index that array, each run's tiles dealt round-robin to its
+    segments."""
+    n = ctypes.c_uint32()
+    tp = tiles.ctypes.data if len(tiles) else None
+    check(lib().nz_plan_work_interleaved(descs.ctypes.data, tp, len(tiles), int(slots), None, 0, ctypes.byref(n), None))
+    segments = np.zeros(n.value, dtype=WORK)
+    order = np.zeros(len(tiles), dtype=np.uint32)
+    check(lib().nz_plan_work_interleaved(descs.ctypes.data, tp, len(tiles), int(slots), segments.ctypes.data, n.value,
+                                         ctypes.byref(n), order.ctypes.data if len(tiles) else None))
+    return segments, order
 
 
 def decode_slots(element_size, bit_reorder, long_codes):

@@ -193,6 +193,22 @@ int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
     });
 }
 
+int nz_plan_work_interleaved(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
+                             nz_work* segments, uint32_t capacity, uint32_t* n_segments, uint32_t* order) {
+    return guarded([&] {
+        if (!frags || (!tiles && n_tiles) || !n_segments) nz::fail(nz::kInvalidArgument, "Null plan argument.");
+        if (segments && n_tiles && !order) nz::fail(nz::kInvalidArgument, "Null tile order argument.");
+        std::vector<uint32_t> perm;
+        const auto plan = nz::plan_work_interleaved(frags, tiles, n_tiles, slots, &perm);
+        *n_segments = static_cast<uint32_t>(plan.size());
+        if (segments) {
+            if (plan.size() > capacity) nz::fail(nz::kInvalidArgument, "Segment buffer is too small.");
+            std::copy(plan.begin(), plan.end(), segments);
+            std::copy(perm.begin(), perm.end(), order);
+        }
+    });
+}
+
 int nz_decode_slots(int element_size, int bit_reorder, int long_codes, int* slots) {
     if (!slots) return set_error(nz::kInvalidArgument, "Null slots argument.");
     char message[256] = {0};

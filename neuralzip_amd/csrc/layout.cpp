@@ -280,14 +280,25 @@ void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
     while (row < rows) row_index[++row] = static_cast<uint32_t>(entries.size());
 }
 
-std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
-    std::vector<nz_work> runs;   // maximal runs of one LUT and kind
-    if (!n_tiles) return runs;
+namespace {
+
+// Maximal runs of one LUT and kind, their costs (elements, raw tiles at half
+// weight) and the workgroups each run gets.
+struct Shares {
+    std::vector<nz_work> runs;
+    std::vector<double> cost;
+    std::vector<uint64_t> share;
+};
+
+Shares share_out(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
+    Shares out;
+    std::vector<nz_work>& runs = out.runs;
+    if (!n_tiles) return out;
     auto key = [&](uint32_t t) {
         const nz_frag_desc& f = frags[tiles[t].frag];
         return std::pair<uint64_t, uint32_t>(f.kind == NZ_KIND_RAW ? 0 : f.lut, f.kind);
     };
-    std::vector<double> cost;
+    std::vector<double>& cost = out.cost;
     uint32_t start = 0;
     double sum = 0;
     for (uint32_t t = 0; t <= n_tiles; ++t) {
@@ -307,7 +318,8 @@ std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, 
     // so it should have at least a tile per wavefront to decode.
     const uint64_t enough = (n_tiles + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
     const uint64_t groups = std::max<uint64_t>(std::min<uint64_t>(slots, enough), n_seg);
-    std::vector<uint64_t> share(n_seg, 1);
+    std::vector<uint64_t>& share = out.share;
+    share.assign(n_seg, 1);
     double total = 0;
     for (double c : cost) total += c;
     if (groups > n_seg && total > 0) {
@@ -325,6 +337,17 @@ std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, 
         std::sort(rest.begin(), rest.end(), [](auto& x, auto& y) { return x.first > y.first || (x.first == y.first && x.second < y.second); });
         for (size_t k = 0; given < extra; ++k, ++given) share[rest[k % n_seg].second] += 1;
     }
+    return out;
+}
+
+}  // namespace
+
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
+    const Shares sh = share_out(frags, tiles, n_tiles, slots);
+    const std::vector<nz_work>& runs = sh.runs;
+    const std::vector<double>& cost = sh.cost;
+    const std::vector<uint64_t>& share = sh.share;
+    const size_t n_seg = runs.size();
     // Cut each run into its share of ranges of about equal cost.
     std::vector<nz_work> ranges;
     for (size_t i = 0; i < n_seg; ++i) {
@@ -345,6 +368,24 @@ std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, 
         }
     }
     return ranges;
+}
+
+std::vector<nz_work> plan_work_interleaved(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                                           uint32_t slots, std::vector<uint32_t>* order) {
+    const Shares sh = share_out(frags, tiles, n_tiles, slots);
+    std::vector<nz_work> segments;
+    order->clear();
+    order->reserve(n_tiles);
+    for (size_t i = 0; i < sh.runs.size(); ++i) {
+        const nz_work& run = sh.runs[i];
+        const uint32_t parts = static_cast<uint32_t>(std::min<uint64_t>(sh.share[i], run.tile1 - run.tile0));
+        for (uint32_t p = 0; p < parts; ++p) {
+            const uint32_t begin = static_cast<uint32_t>(order->size());
+            for (uint32_t t = run.tile0 + p; t < run.tile1; t += parts) order->push_back(t);
+            segments.push_back({begin, static_cast<uint32_t>(order->size()), tiles[run.tile0 + p].frag, run.kind});
+        }
+    }
+    return segments;
 }
 
 namespace {

@@ -59,6 +59,13 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 // contiguous segments of about equal elements.
 std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots);
 
+// The same shares, with each run's tiles dealt round-robin to its segments:
+// segment p of a run of P segments takes the run's tiles p, p + P, p + 2P...
+// *order receives the launch's tile order (the tile array to upload is
+// tiles[order[0]], tiles[order[1]], ...) and the segments index that array.
+std::vector<nz_work> plan_work_interleaved(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                                           uint32_t slots, std::vector<uint32_t>* order);
+
 // Checks a fused product's weight list: 1..NZ_MATVEC_MAX_WEIGHTS weights,
 // aligned offsets in increasing disjoint order, cols a multiple of 16 bytes
 // of elements, under 2^32 stacked elements.

@@ -134,7 +134,9 @@ class HIPDecoder:
         device = store.device
         if slots is None:
             slots = self.slots(device, key)
-        segments = _native.plan_work(store.descs, tiles, slots)
+        # Workgroups running at once work on nearby tiles (round-robin segments).
+        segments, order = _native.plan_work_interleaved(store.descs, tiles, slots)
+        tiles = tiles[order]
         tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
         segments_t = torch.from_numpy(segments.view(np.uint8).copy()).to(device)
         args = (store.buffer.data_ptr(), store.frags.data_ptr(), tiles_t.data_ptr(), segments_t.data_ptr(),

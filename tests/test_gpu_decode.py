@@ -16,10 +16,12 @@ from nz_helpers import Encoded, segment_lengths, segment_tensor, singleton_heade
 pytestmark = pytest.mark.gpu
 
 
-def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, slots=None, launches=2):
+def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, slots=None, launches=2,
+            interleaved=False):
     """Decodes every tile (one launch per kind) `launches` times in a row,
     poisoning the workspace before each round; returns the workspace bytes
-    of every round and the plans."""
+    of every round and the plans. `interleaved` plans with
+    nz_plan_work_interleaved (and uploads the tiles in its order)."""
     device = torch.device("cuda:0")
     out = torch.full((workspace_elements * element_size + 64,), 0xA5, dtype=torch.uint8, device=device)
     base_t = torch.from_numpy(base).to(device)
@@ -32,7 +34,11 @@ def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, s
         if not len(sel):
             continue
         n = slots if slots is not None else _native.decode_slots(element_size, bit_reorder, long_codes)
-        segments = _native.plan_work(descs, sel, n)
+        if interleaved:
+            segments, order = _native.plan_work_interleaved(descs, sel, n)
+            sel = sel[order]
+        else:
+            segments = _native.plan_work(descs, sel, n)
         plans.append((long_codes, sel, segments,
                       [torch.from_numpy(a.view(np.uint8).copy()).to(device) for a in (sel, segments)]))
     rounds = []
@@ -47,13 +53,14 @@ def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, s
     return rounds, plans
 
 
-def check_case(tensors, codebooks, dtype, repeats=1, slots=None):
+def check_case(tensors, codebooks, dtype, repeats=1, slots=None, interleaved=False):
     spec = DTYPES[dtype]
     enc = Encoded(tensors, codebooks)
     base, descs, tiles = enc.host_image()
     size = max(off + raw.size // spec.element_size for raw, _, _, _, off in tensors)
     for _ in range(repeats):
-        rounds, plans = run_gpu(base, descs, tiles, spec.element_size, spec.bit_reorder, size, slots)
+        rounds, plans = run_gpu(base, descs, tiles, spec.element_size, spec.bit_reorder, size, slots,
+                                interleaved=interleaved)
         emu = np.full_like(rounds[0], 0xA5)
         for _, sel, segments, _ in plans:
             _native.emulate_decode(base, descs, sel, segments, spec.element_size, spec.bit_reorder, emu)
@@ -96,6 +103,25 @@ def test_long_code_tiles_decode_the_same_every_time(max_bits, dtype):
     symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
     raw = segment_tensor(dtype, symbols)
     check_case([(raw, dtype, 1 << 20, [0], 0)], {0: book}, dtype, repeats=4)
+
+
+@pytest.mark.parametrize("slots", [None, 3, 100000])
+def test_interleaved_plan_is_bit_exact(slots):
+    """The decode launch's own plan (nz_plan_work_interleaved: round-robin
+    segments over a reordered tile array) on two codebooks, a raw chunk and
+    long codes, against the original words and the CPU emulation."""
+    g = torch.Generator().manual_seed(6)
+    raw = (torch.randn(512, 1500, generator=g) * 0.03).bfloat16().view(torch.uint8).numpy().reshape(-1)
+    books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16)),
+             1: _native.Codebook(singleton_header(raw[:40000], torch.bfloat16, prior=3))}
+    ids = [(0, 1, -1)[j % 3] for j in range(-(-raw.size // 2 // 65536))]
+    check_case([(raw, torch.bfloat16, 65536, ids, 64)], books, torch.bfloat16, slots=slots, interleaved=True)
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(56), vocab)
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
+    long_raw = segment_tensor(torch.float32, symbols)
+    check_case([(long_raw, torch.float32, 1 << 20, [0], 0)], {0: book}, torch.float32, repeats=2, slots=slots,
+               interleaved=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])

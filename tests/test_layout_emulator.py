@@ -5,6 +5,8 @@ decode, ballot-scan staging and vector assembly; these cases mirror
 tests/test_gpu_decode.py so that layout and indexing mistakes show up here
 before a GPU run.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -82,6 +84,45 @@ def test_work_partitions(slots):
     ids = [(0, 1, -1)[j % 3] for j in range(-(-300000 // 65536))]
     emulate_case([(raw, torch.bfloat16, 65536, ids, 128)], books, torch.bfloat16, slots)
 
+
+
+@pytest.mark.parametrize("slots", [1, 5, 64, 100000])
+def test_interleaved_plan(slots):
+    """nz_plan_work_interleaved: the same workgroups per run as nz_plan_work,
+    each run's tiles dealt round-robin to its segments over the reordered
+    tile array, and a decode with that plan is still bit-exact."""
+    g = torch.Generator().manual_seed(4)
+    raw = (torch.randn(300, 1000, generator=g) * 0.05).bfloat16().view(torch.uint8).numpy().reshape(-1)
+    books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16)),
+             1: _native.Codebook(singleton_header(raw[:20000], torch.bfloat16, prior=3))}
+    ids = [(0, 1, -1)[j % 3] for j in range(-(-300000 // 65536))]
+    spec = DTYPES[torch.bfloat16]
+    base, descs, tiles = Encoded([(raw, torch.bfloat16, 65536, ids, 128)], books).host_image()
+    kinds = descs["kind"][tiles["frag"]]
+    luts = np.where(kinds == _native.KIND_RAW, 0, descs["lut"][tiles["frag"]])
+    order_key = np.lexsort((np.arange(len(tiles)), luts, kinds))
+    tiles = tiles[order_key]   # tiles of one LUT and kind adjacent, as prepare_batch orders them
+    contiguous = _native.plan_work(descs, tiles, slots)
+    segments, order = _native.plan_work_interleaved(descs, tiles, slots)
+    assert len(segments) == len(contiguous)
+    assert np.array_equal(np.sort(order), np.arange(len(tiles)))
+    assert segments["tile0"][0] == 0 and segments["tile1"][-1] == len(tiles)
+    assert np.all(segments["tile0"][1:] == segments["tile1"][:-1])
+    for seg in segments:
+        members = order[seg["tile0"]:seg["tile1"]]
+        frags = tiles["frag"][members]
+        assert len(set(descs["kind"][frags])) == 1
+        assert descs["kind"][frags[0]] == _native.KIND_RAW or len(set(descs["lut"][frags])) == 1
+        assert descs["lut"][seg["lut_frag"]] == descs["lut"][frags[0]] and seg["kind"] == descs["kind"][frags[0]]
+        if len(members) > 1:   # every P-th tile of its run
+            assert len(set(np.diff(members.astype(np.int64)))) == 1
+    out = np.full(raw.size + 64 * 2 + 256, 0xA5, dtype=np.uint8)
+    _native.emulate_decode(base, descs, tiles[order], segments, spec.element_size, spec.bit_reorder, out)
+    assert np.array_equal(out[128 * 2:128 * 2 + raw.size], raw)
+    with pytest.raises(_native.NativeError, match="order"):   # segments wanted, no room for the order
+        _native.check(_native.lib().nz_plan_work_interleaved(
+            descs.ctypes.data, tiles.ctypes.data, len(tiles), slots, segments.ctypes.data, len(segments),
+            ctypes.byref(ctypes.c_uint32()), None))
 
 def test_codebook_lengths_match_the_oracle_on_golden_headers():
     import json
