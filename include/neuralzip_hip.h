@@ -133,12 +133,15 @@ int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
                  nz_work* segments, uint32_t capacity, uint32_t* n_segments);
 
 /* The decode launch's plan: the same shares of workgroups as nz_plan_work,
- * but each run's tiles are dealt round-robin to its segments (segment p of
- * a run of P segments takes the run's tiles p, p + P, p + 2P, ...). The
- * tiles to upload for the launch are tiles[order[0]], tiles[order[1]], ...
- * (order: n_tiles entries), and the segments index that array. The
- * workgroups running at once then read and write nearby memory rather than
- * as many far-apart streams as there are workgroups. With segments == NULL
+ * but each run's tiles are dealt round-robin to its segments: each segment
+ * of a run of P segments takes the run's tiles r, r + P, r + 2P, ... for its
+ * own round position r. Neighbouring positions go to segments on one XCD
+ * (launch index mod 8, as MI355X places workgroups), since neighbouring
+ * tiles share cache lines at their edges. The tiles to upload for the
+ * launch are tiles[order[0]], tiles[order[1]], ... (order: n_tiles
+ * entries), and the segments index that array. The workgroups running at
+ * once then read and write nearby memory rather than as many far-apart
+ * streams as there are workgroups. With segments == NULL
  * only *n_segments is set. No counterpart in the reference, whose grid has
  * one CTA per 4 KiB of bitstream (inference.py:183-191, decoder.py:168-179). */
 int nz_plan_work_interleaved(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,

@@ -210,6 +210,7 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 }
 
 constexpr uint64_t kMinTilesPerGroup = 16;
+constexpr size_t kXcds = 8;   // MI355X: accelerator dies, each with its own L2
 
 void check_matvec_group(const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, unsigned element_size) {
     if (element_size != 2 && element_size != 4) fail(kInvalidArgument, "element_size must be 2 or 4.");
@@ -379,10 +380,23 @@ std::vector<nz_work> plan_work_interleaved(const nz_frag_desc* frags, const nz_t
     for (size_t i = 0; i < sh.runs.size(); ++i) {
         const nz_work& run = sh.runs[i];
         const uint32_t parts = static_cast<uint32_t>(std::min<uint64_t>(sh.share[i], run.tile1 - run.tile0));
-        for (uint32_t p = 0; p < parts; ++p) {
+        const size_t first = segments.size();   // launch index of the run's first segment
+        // Round position r (tiles r, r + P, r + 2P... of the run) -> segment.
+        // Neighbouring tiles share cache lines at their edges (a window, a
+        // metadata line, a raw-lane line), so neighbouring positions go to
+        // segments the hardware places on one XCD (one L2): workgroup w runs
+        // on XCD w mod kXcds.
+        std::vector<uint32_t> by_xcd(parts);
+        for (uint32_t q = 0; q < parts; ++q) by_xcd[q] = q;
+        std::stable_sort(by_xcd.begin(), by_xcd.end(),
+                         [&](uint32_t x, uint32_t y) { return (first + x) % kXcds < (first + y) % kXcds; });
+        std::vector<uint32_t> position(parts);   // the round position of each segment
+        for (uint32_t r = 0; r < parts; ++r) position[by_xcd[r]] = r;
+        for (uint32_t q = 0; q < parts; ++q) {
             const uint32_t begin = static_cast<uint32_t>(order->size());
-            for (uint32_t t = run.tile0 + p; t < run.tile1; t += parts) order->push_back(t);
-            segments.push_back({begin, static_cast<uint32_t>(order->size()), tiles[run.tile0 + p].frag, run.kind});
+            for (uint32_t t = run.tile0 + position[q]; t < run.tile1; t += parts) order->push_back(t);
+            segments.push_back({begin, static_cast<uint32_t>(order->size()), tiles[run.tile0 + position[q]].frag,
+                                run.kind});
         }
     }
     return segments;

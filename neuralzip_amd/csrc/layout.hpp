@@ -60,9 +60,11 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots);
 
 // The same shares, with each run's tiles dealt round-robin to its segments:
-// segment p of a run of P segments takes the run's tiles p, p + P, p + 2P...
-// *order receives the launch's tile order (the tile array to upload is
-// tiles[order[0]], tiles[order[1]], ...) and the segments index that array.
+// each segment of a run of P segments takes the run's tiles r, r + P,
+// r + 2P... for its own round position r, and neighbouring positions belong
+// to segments on one XCD (launch index mod 8). *order receives the launch's
+// tile order (the tile array to upload is tiles[order[0]], tiles[order[1]],
+// ...) and the segments index that array.
 std::vector<nz_work> plan_work_interleaved(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
                                            uint32_t slots, std::vector<uint32_t>* order);
 

@@ -108,6 +108,19 @@ def test_interleaved_plan(slots):
     assert np.array_equal(np.sort(order), np.arange(len(tiles)))
     assert segments["tile0"][0] == 0 and segments["tile1"][-1] == len(tiles)
     assert np.all(segments["tile0"][1:] == segments["tile1"][:-1])
+    # neighbouring tiles of a run go to segments on one XCD (launch index mod 8)
+    seg_of = np.empty(len(tiles), dtype=np.int64)
+    for k, seg in enumerate(segments):
+        seg_of[order[seg["tile0"]:seg["tile1"]]] = k
+    keys = list(zip(kinds[order_key].tolist(), luts[order_key].tolist()))
+    runs = [0] + [t for t in range(1, len(keys)) if keys[t] != keys[t - 1]] + [len(keys)]
+    same = total = 0
+    for a, b in zip(runs[:-1], runs[1:]):
+        parts = len(set(seg_of[a:b]))
+        if parts >= 16:
+            same += int(np.sum(seg_of[a:b - 1] % 8 == seg_of[a + 1:b] % 8))
+            total += b - 1 - a
+    assert total == 0 or same >= 0.75 * total
     for seg in segments:
         members = order[seg["tile0"]:seg["tile1"]]
         frags = tiles["frag"][members]
@@ -123,6 +136,29 @@ def test_interleaved_plan(slots):
         _native.check(_native.lib().nz_plan_work_interleaved(
             descs.ctypes.data, tiles.ctypes.data, len(tiles), slots, segments.ctypes.data, len(segments),
             ctypes.byref(ctypes.c_uint32()), None))
+
+
+def test_interleaved_plan_keeps_neighbouring_tiles_on_one_xcd():
+    """Neighbouring tiles share cache lines at their edges; the plan gives
+    them to segments whose launch index agrees mod 8 (the XCD MI355X places
+    them on), except where a round's positions cross from one XCD's segments
+    to the next."""
+    g = torch.Generator().manual_seed(8)
+    raw = (torch.randn(2048, 1024, generator=g) * 0.02).bfloat16().view(torch.uint8).numpy().reshape(-1)
+    book = _native.Codebook(singleton_header(raw, torch.bfloat16))
+    _, descs, tiles = Encoded([(raw, torch.bfloat16, 131072, [0] * 16, 0)], {0: book}).host_image()
+    segments, order = _native.plan_work_interleaved(descs, tiles, 512)
+    parts = len(segments)
+    assert parts >= 64
+    seg_of = np.empty(len(tiles), dtype=np.int64)
+    for k, seg in enumerate(segments):
+        seg_of[order[seg["tile0"]:seg["tile1"]]] = k
+    same = seg_of[:-1] % 8 == seg_of[1:] % 8
+    rounds = -(-len(tiles) // parts)
+    assert int(np.sum(~same)) <= 8 * rounds
+    # and every segment holds every P-th tile
+    for seg in segments:
+        assert set(np.diff(order[seg["tile0"]:seg["tile1"]].astype(np.int64))) <= {parts}
 
 def test_codebook_lengths_match_the_oracle_on_golden_headers():
     import json
