@@ -108,13 +108,19 @@ struct RowSpan {
 
 // Stacked row and column of a tile's staging index 0 (`first`, a workspace
 // element): the weight is the last one of the group starting at or before it.
+// Constant indices only: the group's fields stay in scalar registers and the
+// weight is picked with selects, not with loads at a computed index.
 __device__ __forceinline__ RowSpan row_span(uint64_t first, const nz_matvec_group& g) {
-    uint32_t w = 0;
+    uint64_t offset = g.offset[0];
+    uint32_t row_base = g.row_base[0];
 #pragma unroll
-    for (uint32_t k = 1; k < NZ_MATVEC_MAX_WEIGHTS; ++k)
-        if (k < g.count && first >= g.offset[k]) w = k;
+    for (uint32_t k = 1; k < NZ_MATVEC_MAX_WEIGHTS; ++k) {
+        const bool later = k < g.count && first >= g.offset[k];
+        offset = later ? g.offset[k] : offset;
+        row_base = later ? g.row_base[k] : row_base;
+    }
     const uint32_t cols = g.cols;
-    const uint32_t rel = static_cast<uint32_t>(first - g.offset[w]) + g.row_base[w] * cols;
+    const uint32_t rel = static_cast<uint32_t>(first - offset) + row_base * cols;
     RowSpan s;
     s.row0 = rel / cols;
     s.col0 = rel - s.row0 * cols;
