@@ -2,15 +2,16 @@
 //
 // Replaces decode_batched (neuralzip/gpu/cuda/decode.cu:323-381) with a
 // wave64 design over the layout of nz_format.h:
-//   * one workgroup (8 wavefronts) per contiguous tile range of one
-//     codebook; the codebook's 12-bit multi-token LUT and its escape tables
-//     are staged once in LDS;
+//   * one workgroup (16 wavefronts) per segment: tiles of one codebook
+//     (with the interleaved plan, every P-th tile of the codebook's run);
+//     the codebook's 12-bit multi-token LUT and its escape tables are staged
+//     once in LDS;
 //   * one wavefront per tile, one lane per 64-bit window: the lane restarts
 //     at its stored gap and runs LUT steps until it has emitted its stored
-//     count of exponent bytes (one to three per step; a long code goes
-//     through the canonical escape search), writing them into the
-//     wavefront's LDS staging area at the offset given by a DPP prefix scan
-//     of the counts;
+//     count of exponent bytes (one to four per step; a long code goes
+//     through the canonical escape search), ORing them into the wavefront's
+//     cleared LDS staging area at the offset given by a DPP prefix scan of
+//     the counts;
 //   * the wavefront then merges staged exponents with the raw byte lanes,
 //     undoes the sign/exponent reorder (decode.cu:83-100) with bit-field
 //     inserts, and stores whole 16-byte vectors; the elements of the (at

@@ -3,7 +3,8 @@
 // y[b, n] = sum_k W[n, k] * x[b, k] + bias[n] for up to four row-major
 // weights W (rows x cols each) that share the activations x, stored in the
 // layout of nz_format.h, without writing W anywhere. The weights' rows are
-// stacked in workspace order; a tile finds its weight from its first element. No counterpart in the reference, which always decodes a block
+// stacked in workspace order; a tile finds its weight from its first
+// element. No counterpart in the reference, which always decodes a block
 // into its workspace before the module's own GEMM reads it
 // (neuralzip/gpu/inference.py:379-509).
 //
