@@ -6,6 +6,7 @@ device tensors per chunk (neuralzip/gpu/inference.py:401-432), every
 fragment of an export lives in one packed device buffer (DeviceStore); a
 PreparedBatch holds the tile and workgroup arrays of one launch.
 """
+import ctypes
 from dataclasses import dataclass, field
 from functools import cached_property
 
@@ -191,9 +192,14 @@ class HIPDecoder:
         bits = np.where(raw, numel, (descs["bit_length"].astype(np.int64) + 7) // 8)
         windows = np.where(raw, 0, (descs["bit_length"].astype(np.int64) + WINDOW_BITS - 1) // WINDOW_BITS)
         reads = int(bits.sum() + 2 * windows.sum() + (numel * (dtype.element_size - 1)).sum())
+        launch_weights, reduce_weights = _native.matvec_weights(weights), _native.matvec_weights(weights)
+        es, reorder = dtype.element_size, int(dtype.bit_reorder)
+        launch_args = tuple((store.buffer.data_ptr(), store.frags.data_ptr(), tensors[0].data_ptr(), segments_ptr,
+                             n_segments, es, reorder, long_codes, ctypes.addressof(launch_weights), len(weights),
+                             int(cols)) for segments_ptr, n_segments, long_codes in launches)
+        reduce_args = (tensors[1].data_ptr(), tensors[2].data_ptr(), ctypes.addressof(reduce_weights), len(weights))
         return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, weights, int(cols), len(tiles),
-                              store, tuple(launches), _native.matvec_weights(weights), reads,
-                              _native.matvec_weights(weights))
+                              store, tuple(launches), launch_weights, reads, reduce_weights, launch_args, reduce_args)
 
     def matvec(self, prepared, x, biases=None, partials=None, stream=None):
         """x @ W^T (+ bias) for each weight of the product: x is (batch, cols),
@@ -231,15 +237,15 @@ class HIPDecoder:
             ys.append(block.view(batch, rows))
             reduce_weights[k].y = block.data_ptr()
             reduce_weights[k].bias = None if bias is None else bias.data_ptr()
-        tiles_t, row_index_t, entries_t = prepared.device_tensors[:3]
-        es, reorder = prepared.layout
-        for segments_ptr, n_segments, long_codes in prepared.launches:
-            _native.matvec_launch(prepared.store.buffer.data_ptr(), prepared.store.frags.data_ptr(),
-                                  tiles_t.data_ptr(), segments_ptr, n_segments, es, int(reorder), long_codes,
-                                  prepared.launch_weights, prepared.cols, x.data_ptr(), batch, partials.data_ptr(),
-                                  prepared.n_tiles, stream.cuda_stream)
-        _native.matvec_reduce(row_index_t.data_ptr(), entries_t.data_ptr(), reduce_weights, partials.data_ptr(),
-                              batch, es, int(reorder), stream.cuda_stream)
+        lib, es, reorder = _native.lib(), prepared.layout[0], int(prepared.layout[1])
+        x_ptr, partials_ptr, stream_ptr = x.data_ptr(), partials.data_ptr(), stream.cuda_stream
+        for args in prepared.launch_args:
+            rc = lib.nz_matvec_launch(*args, x_ptr, batch, partials_ptr, prepared.n_tiles, stream_ptr)
+            if rc:
+                _native.check(rc)
+        rc = lib.nz_matvec_reduce(*prepared.reduce_args, partials_ptr, batch, es, reorder, stream_ptr)
+        if rc:
+            _native.check(rc)
         return tuple(ys)
 
     def decode_batch(self, prepared, stream=None):
@@ -272,6 +278,9 @@ class PreparedMatvec:
     # MatvecWeight array of the reduce; each call sets its output and bias
     # pointers (so one plan serves one call at a time)
     reduce_weights: object = field(repr=False, default=None)
+    # the launches' and the reduce's fixed leading arguments, built once
+    launch_args: tuple = field(repr=False, default=())
+    reduce_args: tuple = field(repr=False, default=())
 
     @property
     def rows(self):
