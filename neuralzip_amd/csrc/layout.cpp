@@ -488,6 +488,7 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
                     uint32_t bytes;
                     unsigned n;
                     const unsigned len = lut_step(lut, window, &bytes, &n);
+                    if (n == 0 || len == 0) throw std::runtime_error("LUT step that emits or consumes nothing");
                     const unsigned fill = static_cast<unsigned>(8 * (o & 3));
                     store_or(o & ~3ull, bytes << fill);
                     store_or((o & ~3ull) + 4, fill ? bytes >> (32 - fill) : 0u);
