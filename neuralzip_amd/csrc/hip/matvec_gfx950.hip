@@ -159,15 +159,20 @@ struct Partial {
 template <int ES, bool REORDER, bool LONG, int BT>
 __device__ __forceinline__ void multiply_tile(const TileInfo& ti, const Fetch<ES, LONG>& d, const uint8_t* stage,
                                               const RowSpan& rs, rsrc_t x, uint32_t cols, uint32_t batch,
-                                              uint32_t lane, Partial<BT>& p) {
+                                              uint32_t lane, Partial<BT>& p, const uint4 (&early)[2]) {
     using G = Geometry<ES>;
     constexpr uint32_t V = G::V;
 #pragma unroll
     for (int b = 0; b < BT; ++b) {
-        // the activations of every round first, then one round's weights at a time
+        // the activations of every round first (row 0's first two rounds were
+        // requested before the decode), then one round's weights at a time
         uint4 xv[G::kRounds];
 #pragma unroll
         for (uint32_t r = 0; r < G::kRounds; ++r) {
+            if (b == 0 && r < 2) {
+                xv[r] = early[r];
+                continue;
+            }
             const uint32_t g = (lane + NZ_WAVE * r) * V;
             const bool whole = g >= ti.s0 && g + V <= ti.s1;
             const uint32_t col = rs.col0 + g - (g >= rs.split ? cols : 0u);
@@ -226,21 +231,34 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_fr
     const uint32_t n = seg.tile1 - seg.tile0;
     uint32_t t = claim(counter, lane);
     if (t >= n) return;
+    // The next tile's windows are requested a tile ahead; this tile's raw
+    // lanes and its first activations at its start, so that the decode hides
+    // their latency (holding the next tile's raw lanes as well would not fit
+    // the 64 registers of eight wavefronts per SIMD).
     TileInfo cur = tile_info<ES>(base, frags, tiles, seg.tile0 + t);
     Fetch<ES, LONG> fc;
-    fetch<ES, LONG>(cur, lane, fc);
+    fetch_bits<ES, LONG>(cur, lane, fc);
     uint32_t tn = claim(counter, lane);
     Partial<BT> p;
     for (;;) {
         const bool more = tn < n;
         const TileInfo nxt = tile_info<ES>(base, frags, tiles, seg.tile0 + (more ? tn : t));
         Fetch<ES, LONG> fn;
-        fetch<ES, LONG>(nxt, lane, fn);
+        fetch_bits<ES, LONG>(nxt, lane, fn);
         const uint32_t after = more ? claim(counter, lane) : n;
+        fetch_raw<ES, LONG>(cur, lane, fc);
+        const RowSpan rs = row_span(cur.first, group);
+        uint4 early[2];   // activation row 0 of rounds 0 and 1
+#pragma unroll
+        for (uint32_t r = 0; r < 2; ++r) {
+            const uint32_t g = (lane + NZ_WAVE * r) * Geometry<ES>::V;
+            const bool whole = g >= cur.s0 && g + Geometry<ES>::V <= cur.s1;
+            const uint32_t col = rs.col0 + g - (g >= rs.split ? cols : 0u);
+            early[r] = load_vector(x, whole ? col * ES : kOutOfRange);
+        }
         stage_tile<ES, LONG, ESC>(cur, fc, lut, stage, lane);
         p.clear();
-        multiply_tile<ES, REORDER, LONG, BT>(cur, fc, stage, row_span(cur.first, group), x, cols, batch,
-                                             lane, p);
+        multiply_tile<ES, REORDER, LONG, BT>(cur, fc, stage, rs, x, cols, batch, lane, p, early);
         p.flush(partials, seg.tile0 + t, batch, lane);
         if (!more) break;
         t = tn;

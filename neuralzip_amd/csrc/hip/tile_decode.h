@@ -204,13 +204,11 @@ struct Fetch {
     uint32_t edge;             // raw lane bytes of this lane's edge element
 };
 
+// The part of a tile's data the decode needs first: window metadata and bits.
 template <int ES, bool LONG>
-__device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<ES, LONG>& d) {
-    using G = Geometry<ES>;
+__device__ __forceinline__ void fetch_bits(const TileInfo& ti, uint32_t lane, Fetch<ES, LONG>& d) {
     const rsrc_t meta = make_rsrc(ti.meta, 2 * ti.n_win);
     const rsrc_t bits = make_rsrc(ti.bits, 8 * ti.n_win + NZ_BITS_PAD);
-    const uint32_t span = ti.nv * G::V;   // lane bytes covering the tile's vectors
-    const rsrc_t lanes = make_rsrc(ti.lanes, ES == 2 ? span : 2 * ti.stride + span);
     d.meta = __builtin_amdgcn_raw_buffer_load_b16(meta, 2 * lane, 0, 0);
     {   // the lane's window and the 64 bits after it
         const v4u w = __builtin_amdgcn_raw_buffer_load_b128(bits, 8 * lane, 0, 0);
@@ -219,6 +217,14 @@ __device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<E
         d.w[2] = w.z;
         if (LONG) d.w[3] = w.w;
     }
+}
+
+// The part used only after the decode: raw lanes and the edge elements' bytes.
+template <int ES, bool LONG>
+__device__ __forceinline__ void fetch_raw(const TileInfo& ti, uint32_t lane, Fetch<ES, LONG>& d) {
+    using G = Geometry<ES>;
+    const uint32_t span = ti.nv * G::V;   // lane bytes covering the tile's vectors
+    const rsrc_t lanes = make_rsrc(ti.lanes, ES == 2 ? span : 2 * ti.stride + span);
 #pragma unroll
     for (uint32_t r = 0; r < G::kRounds; ++r) {
         const uint32_t at = (lane + NZ_WAVE * r) * G::V;
@@ -240,6 +246,12 @@ __device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<E
                  (static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(lanes, g + ti.stride, 0, 0)) << 8) |
                  (static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(lanes, g + 2 * ti.stride, 0, 0)) << 16);
     }
+}
+
+template <int ES, bool LONG>
+__device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<ES, LONG>& d) {
+    fetch_bits<ES, LONG>(ti, lane, d);
+    fetch_raw<ES, LONG>(ti, lane, d);
 }
 
 // One LUT step at the head of the window w0..w3: returns the entry (byte
