@@ -205,9 +205,10 @@ class HIPDecoder:
         """x @ W^T (+ bias) for each weight of the product: x is (batch, cols),
         batch <= MATVEC_MAX_BATCH, in the weights' dtype; `biases` is None or
         one bias (or None) per weight; `partials` (fp32, at least
-        2 * n_tiles * batch values) is the first pass's scratch. Returns a
-        tuple of new (batch, rows) tensors, ordered on `stream` (default:
-        current)."""
+        2 * n_tiles * batch values) is the first pass's scratch. Everything
+        runs on `stream` (default: current), where x, the biases and a given
+        `partials` must be ready. Returns a tuple of new (batch, rows)
+        tensors allocated on `stream`."""
         batch = x.shape[0]
         if x.dim() != 2 or x.shape[1] != prepared.cols or not 1 <= batch <= _native.MATVEC_MAX_BATCH:
             raise ValueError(f"matvec input must be (1..{_native.MATVEC_MAX_BATCH}, {prepared.cols}); "
@@ -221,16 +222,21 @@ class HIPDecoder:
             if bias is not None and (bias.dtype != prepared.dtype or bias.numel() != rows or not bias.is_contiguous()
                                      or bias.device != prepared.device):
                 raise ValueError("matvec bias must be contiguous and match the weight's dtype, rows and device.")
-        x = x.contiguous()
         need = 2 * prepared.n_tiles * batch
-        if partials is None:
-            partials = torch.empty(need, dtype=torch.float32, device=prepared.device)
-        elif partials.dtype != torch.float32 or partials.numel() < need or partials.device != prepared.device:
+        if partials is not None and (partials.dtype != torch.float32 or partials.numel() < need
+                                     or partials.device != prepared.device):
             raise ValueError("matvec partials buffer is too small.")
         if stream is None:
             stream = torch.cuda.current_stream(prepared.device)
-        # one allocation; weight k's (batch, rows) output is a contiguous block of it
-        out = torch.empty(batch * prepared.total_rows, dtype=prepared.dtype, device=prepared.device)
+        # The input copy and this call's own buffers are made on `stream`, so
+        # they are ordered before the launches and the caching allocator ties
+        # them to that stream.
+        with torch.cuda.stream(stream):
+            x = x.contiguous()
+            if partials is None:
+                partials = torch.empty(need, dtype=torch.float32, device=prepared.device)
+            # one allocation; weight k's (batch, rows) output is a contiguous block of it
+            out = torch.empty(batch * prepared.total_rows, dtype=prepared.dtype, device=prepared.device)
         blocks = out.split([batch * rows for _, rows in prepared.weights])
         reduce_weights, ys = prepared.reduce_weights, []
         for k, ((_, rows), bias, block) in enumerate(zip(prepared.weights, biases, blocks)):

@@ -321,6 +321,41 @@ def test_runtime_runs_fused_products_for_few_rows_and_decodes_otherwise():
 
 
 @pytest.mark.gpu
+def test_matvec_on_a_side_stream_equals_the_current_stream():
+    """HIPDecoder.matvec on a stream other than the current one, with its
+    input a non-contiguous view (so the call makes its own copy), returns
+    the bits of the same call on the current stream: while the current
+    stream is still busy (the copy must be ordered on the launch stream) and
+    while the launch stream is busy and the current stream allocates and
+    fills small blocks (the call's buffers must not be handed to it)."""
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    model = BlockStack(depth=1).to(torch.bfloat16).eval()
+    setup = NeuralZipSetup().build({n: p.detach() for n, p in model.named_parameters()})
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", matvec_tokens=1)
+    plan = runtime._matvec["layers.0.up"]
+    bias = model.layers[0].up.bias
+    g = torch.Generator().manual_seed(6)
+    wide = torch.randn(2048, 2, generator=g).to(torch.bfloat16).cuda()
+    x = wide.t()[:1]                        # (1, 2048), not contiguous
+    (want,) = runtime._decoder.matvec(plan, x, [bias])
+    torch.cuda.synchronize()
+    current, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    slow = torch.empty(1 << 28, dtype=torch.uint8, device="cuda:0")
+    for busy in (current, side, current, side):
+        side.wait_stream(current)           # x and the bias are ready on the side stream
+        with torch.cuda.stream(busy):
+            slow.fill_(1)
+        (got,) = runtime._decoder.matvec(plan, x, [bias], None, side)
+        for size in (2048, 4096, 8192, 16384, 32768, 65536):
+            for _ in range(4):
+                torch.empty(size, dtype=torch.uint8, device="cuda:0").fill_(0xFF)
+        current.wait_stream(side)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), busy
+        del got
+
+
+@pytest.mark.gpu
 def test_llama_step_after_a_decoded_prefill():
     """Prefill (many rows) decodes and matches bit for bit; a one-token step
     runs the fused products and stays within the rounding of bf16 layers."""
