@@ -351,7 +351,7 @@ class NeuralZipRuntime:
         self.export = exported
         self.device = torch.device(device)
         self.prefetch = bool(prefetch)
-        self.decode_slots = decode_slots   # workgroups per decode launch; None: what the device runs at once
+        self.decode_slots = decode_slots   # workgroups per decode launch; None: one per CU
         self.matvec_tokens = int(matvec_tokens)
         if not 0 <= self.matvec_tokens <= _native.MATVEC_MAX_BATCH:
             raise ValueError(f"matvec_tokens must be in [0, {_native.MATVEC_MAX_BATCH}].")
@@ -393,8 +393,15 @@ class NeuralZipRuntime:
             for f in frags:
                 kinds[int(self.store.descs[f]["kind"]) == KIND_LONG].append(f)
             for long_codes, members in sorted(kinds.items()):
-                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype],
-                                                    slots=decode_slots)
+                slots = decode_slots
+                if slots is None:
+                    # One workgroup per CU. The side-stream decode then shares
+                    # every CU with the compute stream's kernels, and the end
+                    # of one block's launch overlaps the start of the next.
+                    resident = self._decoder.slots(self.device, (spec.element_size, bool(spec.bit_reorder),
+                                                                 bool(long_codes)))
+                    slots = max(1, min(resident, self._compute_units()))
+                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype], slots=slots)
                 self._prepared_batches[name].append(batch)
                 self.algorithmic_bytes[name] = self.algorithmic_bytes.get(name, 0) + batch.algorithmic_bytes
         self._groups_by_block = defaultdict(list)
@@ -443,6 +450,9 @@ class NeuralZipRuntime:
         if plans:
             need = max(2 * plan.n_tiles for plan in plans.values()) * self.matvec_tokens
             self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+
+    def _compute_units(self):
+        return torch.cuda.get_device_properties(self.device).multi_processor_count
 
     @staticmethod
     def _version_of(tensor):
