@@ -93,3 +93,37 @@ def test_prefetch_uses_distinct_slots_and_side_stream():
         for block in model.blocks:
             y = block(y)
         assert exact(y, expected)
+
+
+@pytest.mark.parametrize("decode_slots", [None, 512, 3])
+def test_block_launch_workgroups(decode_slots):
+    """Block launches use one workgroup per CU by default, or the count
+    asked for; every count decodes the same bits."""
+    from neuralzip_amd import _native
+    model = nn.Module()
+    model.blocks = nn.ModuleList([nn.Sequential(nn.Linear(4096, 4096, bias=False, dtype=torch.bfloat16),
+                                                nn.Linear(4096, 4096, bias=False, dtype=torch.bfloat16))
+                                  for _ in range(2)])
+    g = torch.Generator().manual_seed(9)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    named = {n: p.detach().clone() for n, p in model.named_parameters()}
+    reference = copy.deepcopy(model).cuda()
+    x = torch.randn(4, 4096, generator=g).to(torch.bfloat16).cuda()
+    expected = reference.blocks[1](reference.blocks[0](x))
+    setup = NeuralZipSetup().build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0",
+                                      decode_slots=decode_slots)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    resident = _native.decode_slots(2, 1, 0)
+    for batches in runtime._prepared_batches.values():
+        for batch in batches:
+            if decode_slots is None:
+                assert 1 < batch.n_segments <= min(cus, resident)
+            elif decode_slots == 3:   # a launch has at least one segment per codebook run
+                assert batch.n_segments <= max(3, len(runtime.export.codebooks) + 1)
+            else:
+                assert min(cus, resident) < batch.n_segments <= decode_slots
+    for _ in range(3):
+        assert exact(model.blocks[1](model.blocks[0](x)), expected)
