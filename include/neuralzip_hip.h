@@ -232,7 +232,7 @@ int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const n
 /* Huff0 tree description for a 256-bin histogram plus `prior_count` per
  * symbol, code lengths limited to max_bits (<= 12). With header == NULL only
  * *header_size is set. Replaces: _huff0_cpp.build_codebook_from_counts
- * (binding_helpers.h:250-324 -> codebooks.h:1-42). Byte equality with Zstd's
+ * (binding_helpers.h:9-83 -> codebooks.h:1-42). Byte equality with Zstd's
  * table construction is not claimed; the description is format-valid. */
 int nz_huff0_build(const uint64_t* counts256, uint32_t prior_count, uint32_t max_bits,
                    uint8_t* header, size_t capacity, size_t* header_size);

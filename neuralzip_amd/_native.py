@@ -30,6 +30,8 @@ WORK = np.dtype([("tile0", "<u4"), ("tile1", "<u4"), ("lut_frag", "<u4"), ("kind
 assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16
 
 KIND_RAW, KIND_SHORT, KIND_LONG = 0, 1, 2
+# Words of the kernels' LDS copy of a LUT image (NZ_LUT_MAX_WORDS of nz_format.h).
+LUT_MAX_WORDS = 4 + 2 * 4096 + 6 * 56 + 512
 
 
 class NativeError(RuntimeError):

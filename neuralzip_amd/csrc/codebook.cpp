@@ -301,31 +301,50 @@ void build_lut(Codebook& book) {
     }
     for (size_t i = 0; i < esc.size(); ++i)
         tokens[i] = (book.token_bytes[esc[i]] & 0xFFFFu) | (Codebook::token_width(esc[i]) << NZ_ENTRY_COUNT);
+    check_lut_image(lut);
 }
 
 }  // namespace
 
+void check_lut_image(const std::vector<uint32_t>& lut) {
+    constexpr size_t kPrimaryEnd = NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
+    if (lut.size() < kPrimaryEnd || lut[2] != lut.size() || lut.size() > NZ_LUT_MAX_WORDS ||
+        lut.size() != kPrimaryEnd + size_t(NZ_ESC_RECORD) * lut[0] + lut[1])
+        fail(kLayoutLimit, "LUT image size does not match its header or exceeds the LDS copy.");
+}
+
+// Every word this step reads is checked against the image: the kernel's LDS
+// copy of an image is followed by other LDS data (staging areas), so an index
+// past the image would read those instead of failing.
 unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* bytes, unsigned* count) {
     const uint32_t x = static_cast<uint32_t>(window >> (64 - NZ_LUT_BITS));
-    const uint32_t e = lut[NZ_LUT_HEADER + 2 * x], e1 = lut[NZ_LUT_HEADER + 2 * x + 1];
+    const uint32_t e = lut.at(NZ_LUT_HEADER + 2 * x), e1 = lut.at(NZ_LUT_HEADER + 2 * x + 1);
     if (e >> NZ_ENTRY_COUNT) {
         *bytes = e1;
         *count = e >> NZ_ENTRY_COUNT;
         return 32u - (e & NZ_ENTRY_SHIFT_MASK);
     }
-    const unsigned n_len = lut[0];
-    const uint32_t* record = lut.data() + NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
+    const unsigned n_len = lut.at(0), n_tokens = lut.at(1);
+    const size_t record = NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES;
+    const size_t tokens = record + size_t(NZ_ESC_RECORD) * n_len;
+    if (n_len == 0 || tokens + n_tokens > lut.size())
+        fail(kCorruptStream, "Escape entry of a table without escape records.");
+    auto word = [&](size_t k, unsigned field) { return lut.at(record + size_t(NZ_ESC_RECORD) * k + field); };
     unsigned k = 0;
     while (k + 1 < n_len) {
-        const uint64_t limit = record[NZ_ESC_RECORD * k] | static_cast<uint64_t>(record[NZ_ESC_RECORD * k + 1]) << 32;
+        const uint64_t limit = word(k, 0) | static_cast<uint64_t>(word(k, 1)) << 32;
         if (window < limit) break;
         ++k;
     }
-    const uint32_t* r = record + NZ_ESC_RECORD * k;
-    const uint64_t first = r[2] | static_cast<uint64_t>(r[3]) << 32;
-    const unsigned L = r[5];
-    const uint32_t index = r[4] + static_cast<uint32_t>((window - first) >> (64 - L));
-    const uint32_t te = record[NZ_ESC_RECORD * n_len + index];
+    const uint64_t first = word(k, 2) | static_cast<uint64_t>(word(k, 3)) << 32;
+    const unsigned L = word(k, 5);
+    if (L <= NZ_LUT_BITS || L > 56 || window < first)
+        fail(kCorruptStream, "Escape search left its code-length record.");
+    const uint64_t offset = (window - first) >> (64 - L);
+    const uint64_t end = k + 1 < n_len ? word(k + 1, 4) : n_tokens;   // tokens of length L end here
+    if (word(k, 4) + offset >= end)
+        fail(kCorruptStream, "Escape token index past its code length's tokens.");
+    const uint32_t te = lut.at(tokens + word(k, 4) + offset);
     *bytes = te & 0xFFFFu;
     *count = te >> NZ_ENTRY_COUNT;
     return L;

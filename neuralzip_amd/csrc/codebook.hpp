@@ -55,9 +55,15 @@ Codebook build_codebook(const uint8_t* header, size_t header_size,
 // symbols 0..255 (0 = absent) and the description's byte size.
 std::array<uint8_t, 256> huff0_lengths(const uint8_t* header, size_t size, size_t* used);
 
+// Throws unless the image's header words agree with its size and the image
+// fits the kernels' LDS copy (NZ_LUT_MAX_WORDS).
+void check_lut_image(const std::vector<uint32_t>& lut);
+
 // Decoder step at the head of a 64-bit window (MSB first): returns consumed
 // bits and writes the emitted bytes (1..4, first byte lowest) into *bytes /
-// *count. Uses the LUT image exactly as the kernel does.
+// *count. Uses the LUT image exactly as the kernel does, and throws if any
+// word it would read lies outside the image or outside the escape record
+// and token range that the window selects.
 unsigned lut_step(const std::vector<uint32_t>& lut, uint64_t window, uint32_t* bytes,
                   unsigned* count);
 

@@ -3,7 +3,7 @@
 // Storage v2 keeps the selected lane of each chunk as raw bytes, a Huff0
 // 4-stream block (Zstd's format, RFC 8878 4.2) or an NZM1 frame
 // (neuralzip/native/mixed_huffman.h:117-240). This file provides:
-//   * Huff0 tables from histograms (binding_helpers.h:250-324, codebooks.h:1-42):
+//   * Huff0 tables from histograms (binding_helpers.h:9-83, codebooks.h:1-42):
 //     counts are scaled like the reference, lengths are limited to max_bits
 //     with the adjustment of ITU-T T.81 Annex K.3, and the tree description
 //     is written with FSE-compressed or 4-bit weights;
@@ -277,7 +277,7 @@ std::vector<uint8_t> huff0_header_from_lengths(const std::array<uint8_t, 256>& l
 
 std::vector<uint8_t> huff0_build(const uint64_t* counts, uint32_t prior, unsigned max_bits) {
     if (max_bits < 1 || max_bits > 12) fail(kInvalidArgument, "max_bits must be in [1, 12].");
-    // parse_symbol_counts (binding_helpers.h:250-307): scale so the prior
+    // parse_symbol_counts (binding_helpers.h:9-66): scale so the prior
     // plus the histogram stays below 2^30, keeping observed symbols >= 1
     constexpr uint64_t kTotalLimit = (uint64_t(1) << 30) - 1;
     uint64_t total = 0;

@@ -209,7 +209,9 @@ void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
         return;
     }
     const uint4* img = reinterpret_cast<const uint4*>(base + frags[seg.lut_frag].lut);
-    const uint32_t words = reinterpret_cast<const uint32_t*>(img)[2];
+    // the host checks every image against NZ_LUT_MAX_WORDS; the clamp keeps a
+    // malformed one from overwriting the staging areas behind s_lut
+    const uint32_t words = min(reinterpret_cast<const uint32_t*>(img)[2], uint32_t(NZ_LUT_MAX_WORDS));
     uint4* dst = reinterpret_cast<uint4*>(s_lut);
     for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kThreads) dst[i] = img[i];
     __syncthreads();

@@ -431,7 +431,9 @@ void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_til
         std::vector<uint32_t> lut;
         if (work[wi].kind != NZ_KIND_RAW) {
             const uint32_t* img = reinterpret_cast<const uint32_t*>(base + lf.lut);
+            if (img[2] > NZ_LUT_MAX_WORDS) fail(kLayoutLimit, "LUT image exceeds the kernels' LDS copy.");
             lut.assign(img, img + img[2]);
+            check_lut_image(lut);
         }
         for (uint32_t t = work[wi].tile0; t < work[wi].tile1; ++t) {
             const nz_tile& tile = tiles[t];

@@ -478,6 +478,11 @@ class NeuralZipRuntime:
             plan = self._decoder.prepare_matvec(self.store, [i[3] for _, i in ordered], spec, cols)
         except (_native.NativeError, ValueError):
             return
+        # a group's product has the tiles of all its members: the partial-sum
+        # buffer, sized for the largest single Linear, may be too small
+        need = 2 * plan.n_tiles * self.matvec_tokens
+        if self._partials.numel() < need:
+            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
         self._group_plans[first] = (plan, tuple(n for n, _ in ordered),
                                     tuple(self.model.get_submodule(n) for n, _ in ordered))
 

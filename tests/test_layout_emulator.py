@@ -315,3 +315,69 @@ def test_overrun_bytes_must_be_the_next_windows():
     counts[counts >= 2] -= 1   # (a trailing window may hold no code)
     with pytest.raises(Exception, match="past its count"):
         _native.emulate_decode(base, descs, tiles, segments, spec.element_size, spec.bit_reorder, out)
+
+
+@pytest.mark.parametrize("max_bits", [33, 56])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_every_lut_and_escape_index_stays_inside_the_image(max_bits, dtype):
+    """The long-code cases that once decoded wrongly on the GPU: each LUT
+    step of the emulator (the kernel's own step) checks every word it reads
+    against the image's primary table, the escape record the window selects
+    and that record's token range; any index past them raises."""
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(max_bits), vocab)
+    lut = book.lut()
+    assert lut[2] == lut.size <= _native.LUT_MAX_WORDS
+    assert lut.size == 4 + 2 * 4096 + 6 * int(lut[0]) + int(lut[1])
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
+    emulate_case([(segment_tensor(dtype, symbols), dtype, 1 << 20, [0], 0)], {0: book}, dtype)
+
+
+def test_escape_index_past_its_length_raises():
+    """A planted error in the image (the first escape record's token base
+    moved past the tokens) must be caught by the emulator's bounds checks,
+    not read as data."""
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(33), vocab)
+    spec = DTYPES[torch.bfloat16]
+    symbols = np.array([127] * 3000 + list(range(256)) + [125, 126], dtype=np.uint8)
+    raw = segment_tensor(torch.bfloat16, symbols)
+    base, descs, tiles = Encoded([(raw, torch.bfloat16, 1 << 20, [0], 0)], {0: book}).host_image()
+    segments = _native.plan_work(descs, tiles, 512)
+    out = np.zeros(raw.size + 64, dtype=np.uint8)
+    _native.emulate_decode(base, descs, tiles, segments, spec.element_size, spec.bit_reorder, out)
+    assert np.array_equal(out[:raw.size], raw)
+    image = base[int(descs["lut"][0]):].view(np.uint32)
+    record = 4 + 2 * 4096
+    image[record + 4] = int(image[1])     # token base of the first escape length: past every token
+    with pytest.raises(Exception, match="Escape token index"):
+        _native.emulate_decode(base, descs, tiles, segments, spec.element_size, spec.bit_reorder, out)
+
+
+def test_bench_shaped_clusters_stay_inside_their_images():
+    """Eight tensors with the bench workload's statistics (std cycling over
+    five values, 0.1 % Student-t outliers, JS threshold 0.05), scaled down:
+    every codebook's image and every step of every tile pass the checks."""
+    from neuralzip_amd.setup import NeuralZipSetup
+    from neuralzip_amd.gpu.inference import export_tensors_for_gpu
+    g = torch.Generator().manual_seed(1)
+    shapes = [(256, 256), (256, 896), (896, 256), (64, 256), (64, 256), (256, 256), (896, 256), (256, 896)]
+    stds = (0.005, 0.01, 0.02, 0.05, 0.1)
+    named = {}
+    for i, shape in enumerate(shapes):
+        w = torch.randn(shape, generator=g) * stds[i % 5]
+        mask = torch.rand(shape, generator=g) < 1e-3
+        w[mask] = stds[i % 5] * torch.distributions.StudentT(3.0).sample(shape)[mask]
+        named[f"layers.{i}.weight"] = w.bfloat16()
+    setup = NeuralZipSetup(cluster_js_threshold=0.05, chunk_size=32768).build(named)
+    exported = export_tensors_for_gpu(named, setup)
+    assert len(exported.codebooks) >= 2
+    for book in exported.codebooks.values():
+        lut = book.lut()
+        assert lut[2] == lut.size <= _native.LUT_MAX_WORDS
+    spec = DTYPES[torch.bfloat16]
+    for layout, ids, offset, config, name in exported.tensors:
+        books = {i: exported.codebooks[i].native for i in set(ids) if i != -1}
+        raw = named[name].view(torch.uint8).numpy().reshape(-1)
+        step = 32768 // 2
+        emulate_case([(raw, torch.bfloat16, step, list(ids), 0)], books, torch.bfloat16)

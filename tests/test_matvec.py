@@ -384,6 +384,45 @@ def test_llama_step_after_a_decoded_prefill():
     assert err < 2 ** -6, f"relative error {err:.3g}"
 
 
+@pytest.mark.gpu
+def test_grouped_products_after_the_first_step_fit_their_partials():
+    """q/k/v and gate/up are learned as grouped products on the first fused
+    step and used from the second on; a group has the tiles of all its
+    members, more than the largest single Linear here (lm_head is small), so
+    the partial sums must grow. Four one-token steps at batch 2 with
+    matvec_tokens 2 must run and track the bf16 model."""
+    import copy
+    import transformers
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
+    from neuralzip_amd.setup import NeuralZipSetup
+    config = transformers.LlamaConfig(hidden_size=1024, intermediate_size=4096, num_hidden_layers=2,
+                                      num_attention_heads=8, num_key_value_heads=2, vocab_size=256,
+                                      max_position_embeddings=128, tie_word_embeddings=False)
+    torch.manual_seed(3)
+    model = transformers.LlamaForCausalLM(config).to(torch.bfloat16).eval()
+    reference = copy.deepcopy(model).cuda()
+    setup = NeuralZipSetup().build(model)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", matvec_tokens=2)
+    single = max(2 * plan.n_tiles for plan in runtime._matvec.values()) * 2
+    ids = torch.randint(0, 256, (2, 16), generator=torch.Generator().manual_seed(4)).cuda()
+    with torch.no_grad():
+        ref = reference(ids, use_cache=True)
+        got = model(ids, use_cache=True)
+        assert torch.equal(got.logits.view(torch.int16), ref.logits.view(torch.int16))
+        ref_cache, got_cache = ref.past_key_values, got.past_key_values
+        step = ref.logits[:, -1:].argmax(-1)
+        for _ in range(4):
+            r = reference(step, past_key_values=ref_cache)
+            o = model(step, past_key_values=got_cache)
+            ref_cache, got_cache = r.past_key_values, o.past_key_values
+            err = (o.logits.float() - r.logits.float()).norm() / r.logits.float().norm()
+            assert err < 2 ** -5, f"relative error {err:.3g}"
+            step = r.logits[:, -1:].argmax(-1)
+    assert runtime._group_plans, "no grouped product was learned"
+    grouped = max(2 * plan.n_tiles for plan, _, _ in runtime._group_plans.values()) * 2
+    assert grouped > single and runtime._partials.numel() >= grouped
+
+
 class Widening(torch.nn.Module):
     """A block whose input has one row per token but whose Linear sees three."""
 
