@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 5
+#define NZ_ABI_VERSION 6
 
 enum nz_status {
     NZ_OK = 0,
@@ -270,6 +270,16 @@ typedef struct {
     const int32_t* chunk_modes;         /* 0 raw, 1 shared_huff0, 2 mixed_huffman */
 } nz_storage_tensor;
 
+/* The stored form of one selected-lane chunk of `length` symbols under the
+ * storage encoder's rule: *stored_mode receives `mode` when the codebook's
+ * block fits the chunk's budget and saves min_saving_bytes, else 0 (raw),
+ * and *stored_bytes the payload size. Replaces: the per-sample
+ * compress_direct_storage calls of NeuralZipSetup._compare_codebooks
+ * (setup.py:207-249), which read only the selected lane's chunk records. */
+int nz_storage_chunk_size(const nz_codebook* codebook, int mode, const uint8_t* symbols, size_t length,
+                          uint64_t min_saving_bytes, double compression_threshold, int32_t* stored_mode,
+                          uint64_t* stored_bytes);
+
 typedef struct {                        /* one (tensor, lane, chunk) record     */
     int32_t mode;                       /* 0 raw, 1 shared_huff0, 2 mixed_huffman */
     int32_t reserved;
@@ -307,6 +317,44 @@ typedef struct {
  * below 512 KiB). Replaces: _huff0_cpp.decompress_mixed_streams_many
  * (decode_queue.h:1-113); used when loading storage checkpoints. */
 int nz_storage_decompress(const nz_storage_decode_tensor* tensors, size_t count, int threads);
+
+/* ---- setup statistics (host) ------------------------------------------ */
+
+typedef struct {
+    uint32_t element_size;              /* 2 or 4                               */
+    uint32_t bit_reorder;               /* 1: the selected lane is the exponent field */
+    uint32_t mantissa_bits;
+    uint32_t exponent_bits;
+} nz_lane_layout;
+
+/* Per-chunk histograms of one tensor's words (chunks of chunk_elements):
+ * field_counts receives n_chunks x 256 counts of the exponent field
+ * ((word >> mantissa_bits) & mask); lane_counts (256, optional) the counts of
+ * the selected lane's byte over the whole tensor (the exponent field itself
+ * when bit_reorder, else the high byte). Threads as nz_storage_decompress.
+ * Replaces: the per-chunk bincounts of NeuralZipSetup._cluster_chunks
+ * (setup.py:91-141: exponent histogram per chunk, pooled lane counts per
+ * tensor). */
+int nz_chunk_histograms(const uint8_t* words, uint64_t numel, const nz_lane_layout* layout,
+                        uint64_t chunk_elements, int threads, uint32_t* field_counts,
+                        uint64_t* lane_counts);
+
+typedef struct nz_clusterer nz_clusterer;
+
+/* Greedy Jensen-Shannon clustering state (setup.py:91-141): clusters of
+ * chunks of one kind (dtype) and forced label; a chunk without a label
+ * starts a new cluster when its distance to the nearest compatible centroid
+ * exceeds js_threshold; shared == 0 gives every chunk its own cluster. */
+int nz_clusterer_create(double js_threshold, int shared, nz_clusterer** out);
+void nz_clusterer_destroy(nz_clusterer* clusterer);
+
+/* Assigns n chunks, in order, to clusters: field_counts as written by
+ * nz_chunk_histograms, labels[i] the chunk's forced label or -1 (NULL: none),
+ * weights[i] its element count; assignment[i] receives the cluster index
+ * (clusters are numbered in order of creation). */
+int nz_clusterer_assign(nz_clusterer* clusterer, const uint32_t* field_counts, uint64_t n, int32_t kind,
+                        const int64_t* labels, const uint64_t* weights, int32_t* assignment);
+int nz_clusterer_count(const nz_clusterer* clusterer, uint32_t* n_clusters);
 
 #ifdef __cplusplus
 }

@@ -54,13 +54,18 @@ class _FragmentInfo(ctypes.Structure):
                 ("n_tiles", ctypes.c_uint32), ("kind", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
 
 
+class _LaneLayout(ctypes.Structure):
+    _fields_ = [("element_size", ctypes.c_uint32), ("bit_reorder", ctypes.c_uint32),
+                ("mantissa_bits", ctypes.c_uint32), ("exponent_bits", ctypes.c_uint32)]
+
+
 class _Totals(ctypes.Structure):
     _fields_ = [("packed_bytes", ctypes.c_uint64), ("n_fragments", ctypes.c_uint64), ("n_tiles", ctypes.c_uint64)]
 
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 5
+ABI_VERSION = 6
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
@@ -98,6 +103,12 @@ def lib():
         L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, u32,
                                        vp, u32, vp, u32, vp]
         L.nz_matvec_reduce.argtypes = [vp, vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp]
+        L.nz_chunk_histograms.argtypes = [vp, u64, ctypes.POINTER(_LaneLayout), u64, ctypes.c_int, vp, vp]
+        L.nz_clusterer_create.argtypes = [ctypes.c_double, ctypes.c_int, ctypes.POINTER(vp)]
+        L.nz_clusterer_destroy.argtypes = [vp]
+        L.nz_clusterer_destroy.restype = None
+        L.nz_clusterer_assign.argtypes = [vp, vp, u64, ctypes.c_int32, vp, vp, vp]
+        L.nz_clusterer_count.argtypes = [vp, ctypes.POINTER(u32)]
         _lib = L
     return _lib
 
@@ -286,3 +297,52 @@ def matvec_reduce(row_index_ptr, entries_ptr, weights, partials_ptr, batch, elem
     """`weights`: a MatvecWeight array whose y (and bias) pointers are set."""
     check(lib().nz_matvec_reduce(row_index_ptr, entries_ptr, ctypes.cast(weights, ctypes.c_void_p), len(weights),
                                  partials_ptr, int(batch), int(element_size), int(bit_reorder), stream_ptr))
+
+
+def chunk_histograms(words, spec, chunk_elements, *, threads=0, lane_counts=True):
+    """Exponent-field histogram of every chunk of a tensor's words ((chunks, 256)
+    uint32) and, with `lane_counts`, the selected lane's byte counts over the
+    whole tensor (256 uint64)."""
+    words = np.ascontiguousarray(words).reshape(-1).view(np.uint8)
+    numel = words.size // spec.element_size
+    n_chunks = -(-numel // chunk_elements)
+    fields = np.empty((n_chunks, 256), dtype=np.uint32)
+    lanes = np.zeros(256, dtype=np.uint64) if lane_counts else None
+    layout = _LaneLayout(spec.element_size, spec.bit_reorder, spec.mantissa_bits, spec.exponent_mask.bit_length())
+    check(lib().nz_chunk_histograms(words.ctypes.data if words.size else None, numel, ctypes.byref(layout),
+                                    chunk_elements, threads, fields.ctypes.data if fields.size else None,
+                                    lanes.ctypes.data if lanes is not None else None))
+    return fields, lanes
+
+
+class Clusterer:
+    """The setup's greedy Jensen-Shannon chunk clustering (nz_clusterer_*)."""
+
+    def __init__(self, js_threshold, shared=True):
+        handle = ctypes.c_void_p()
+        check(lib().nz_clusterer_create(float(js_threshold), int(bool(shared)), ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def __del__(self):
+        if getattr(self, "handle", None) and _lib is not None:
+            _lib.nz_clusterer_destroy(self.handle)
+            self.handle = None
+
+    def assign(self, field_counts, kind, labels, weights):
+        """Cluster index of each chunk (rows of field_counts), in order."""
+        counts = np.ascontiguousarray(field_counts, dtype=np.uint32)
+        n = counts.shape[0]
+        labels = np.ascontiguousarray(labels, dtype=np.int64)
+        weights = np.ascontiguousarray(weights, dtype=np.uint64)
+        if labels.shape != (n,) or weights.shape != (n,):
+            raise ValueError("One label and one weight per chunk are required.")
+        out = np.empty(n, dtype=np.int32)
+        check(lib().nz_clusterer_assign(self.handle, counts.ctypes.data if n else None, n, int(kind),
+                                        labels.ctypes.data if n else None, weights.ctypes.data if n else None,
+                                        out.ctypes.data if n else None))
+        return out
+
+    def __len__(self):
+        n = ctypes.c_uint32()
+        check(lib().nz_clusterer_count(self.handle, ctypes.byref(n)))
+        return n.value

@@ -13,9 +13,11 @@ LIBRARY = HERE / "libneuralzip_hip.so"
 ARCH = os.environ.get("NZ_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HOST_SOURCES = ("codebook.cpp", "layout.cpp", "codec.cpp", "capi.cpp", "capi_storage.cpp")
+HOST_SOURCES = ("codebook.cpp", "layout.cpp", "codec.cpp", "capi.cpp", "capi_storage.cpp", "survey.cpp")
 DEVICE_SOURCES = ("hip/decode_gfx950.hip", "hip/matvec_gfx950.hip")
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", str(CSRC), "-I", str(ROOT / "include")]
+# host float arithmetic (the setup's clustering) is evaluated as written: no fused multiply-add
+HOST_FLAGS = ["-ffp-contract=off"]
 # packed FP32 instructions stay disabled on every HIP translation unit
 DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
@@ -25,7 +27,7 @@ def build(verbose=False):
     jobs, objects = [], []
     for name in HOST_SOURCES:
         obj = OBJ / (Path(name).stem + ".o")
-        jobs.append(["g++", *COMMON, "-c", str(CSRC / name), "-o", str(obj)])
+        jobs.append(["g++", *COMMON, *HOST_FLAGS, "-c", str(CSRC / name), "-o", str(obj)])
         objects.append(obj)
     for name in DEVICE_SOURCES:
         obj = OBJ / (Path(name).stem + ".o")

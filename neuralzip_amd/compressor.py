@@ -1,8 +1,28 @@
-"""NeuralZipCompressor: transfer plan, storage encode and CPU storage decode
-(neuralzip/compressor.py:16-187)."""
-from dataclasses import replace
+"""NeuralZipCompressor: the setup's transfer plan, storage v2 encode and the
+CPU storage decode (the roles of neuralzip/compressor.py).
+
+Transfer plan. For every tensor being stored or exported to the GPU, one
+codebook id per chunk (-1: the chunk stays raw), resolved from the setup in
+this order:
+  1. the tensor's own chunk assignment, when the setup saw a tensor of this
+     name (or, for `lm_head.weight`, the input embedding it is often tied
+     to), dtype and lane with the same element count;
+  2. that tensor's pooled fallback code for every chunk;
+  3. a global code of the dtype and lane, when one is loaded;
+  4. raw.
+The storage encoder and the GPU export (`gpu/inference.py`) read the same
+plan, so a model exported after loading a checkpoint codes every chunk
+with the codebook its checkpoint used.
+
+Decode. Storage v2 tensors are decoded on the CPU by the native storage
+decoder in batches of at most `direct_batch_bytes` of output; decode tables
+are cached by codebook content, so loading several checkpoints made with
+one setup parses each codebook once.
+"""
+from dataclasses import dataclass
 from pathlib import Path
 
+import numpy as np
 import torch
 
 from neuralzip_amd import huff0
@@ -10,10 +30,18 @@ from neuralzip_amd.dtypes import DTYPES
 from neuralzip_amd.payloads import CodebookPayload
 from neuralzip_amd.setup import NeuralZipSetup
 from neuralzip_amd.storage import _pack_codebooks, pack_direct_storage, unpack_storage
-from neuralzip_amd.utils import _stream_chunk_size, _tensor_from_raw_bytes, time_call
+from neuralzip_amd.utils import _stream_chunk_size, _tensor_from_raw_bytes, tensor_words, time_call
 
-# A tied or absent lm_head reuses the embedding's plan (compressor.py:13).
-_TRANSFER_NAME_FALLBACKS = {"lm_head.weight": ("model.embed_tokens.weight",)}
+# Alternative setup entries for a tensor name, tried after the name itself
+# (a tied or re-created lm_head takes the embedding's codes).
+_PLAN_ALIASES = {"lm_head.weight": ("model.embed_tokens.weight",)}
+_SPECS_BY_NAME = {spec.name: spec for spec in DTYPES.values()}
+
+
+@dataclass(frozen=True)
+class _LanePlan:
+    fallback: int            # codebook id of chunks without an assignment, -1 for raw
+    chunks: np.ndarray       # int64 codebook id per chunk, -1 for raw
 
 
 class NeuralZipCompressor:
@@ -24,149 +52,165 @@ class NeuralZipCompressor:
         self.compression_threshold = setup.compression_threshold
         self.threads = int(threads)
         self.direct_batch_bytes = int(direct_batch_bytes)
-        self._codebook_payloads = list(setup.codebooks)
-        modes = {
-            book.codebook_id: {"kind": book.mode, "codebook_id": book.codebook_id,
-                               "codebook": huff0.build_codebook_from_header(book.codebook, vocab=book.vocab)}
-            for book in setup.codebooks
-        }
-
-        def mode(codebook_id):
-            return {"kind": "raw"} if codebook_id is None else modes[codebook_id]
-
-        self._chunk_modes = {key: tuple(mode(i) for i in ids) for key, ids in setup.chunk_codebooks.items()}
-        self._mode_by_tensor_stream = {key: mode(i) for key, i in setup.tensor_codebooks.items()}
-        self._global_modes = {key: mode(i) for key, i in setup.global_codebooks.items()}
-        self._transfer_mode_by_tensor_stream = {}
-        self._transfer_chunk_modes = {}
+        self._setup = setup
+        self._payloads = {int(book.codebook_id): book for book in setup.codebooks}
+        self._globals = {key: value for key, value in setup.global_codebooks.items()}
+        self._encoders = {}      # codebook id -> parsed table for encoding
+        self._decoders = {}      # (mode, header, vocab) -> parsed table for decoding
+        self._plans = {}
         if gpu:
-            self._add_global_codebooks()
-        self.load_codebooks(self._codebook_payloads)
+            self._load_global_codebooks()
 
-    def encode(self, named_tensors):
-        named_tensors = tuple(named_tensors)
-        self._add_global_codebooks()
-        self.prepare_storage_transfer_target(named_tensors)
-        encoded, seconds = time_call(self._encode, named_tensors)
-        return *encoded, seconds
-
-    def decode(self, blob, metadata):
-        codebooks, payloads = unpack_storage(blob, metadata)
-        self.load_codebooks(codebooks)
-        tensors = self._decompress_tensors(payloads)
-        return {payload.name: tensor for payload, tensor in zip(payloads, tensors, strict=True)}
-
-    def _encode(self, named_tensors):
-        specs, used = [], set()
-        for name, tensor in named_tensors:
-            config = DTYPES[tensor.dtype]
-            stream = config.selected_stream
-            modes = self._transfer_chunk_modes[self._transfer_plan_key(name, tensor, stream)]
-            used.update(m["codebook_id"] for m in modes if m["kind"] != "raw")
-            original = tensor.detach().cpu().contiguous()
-            specs.append((original.reshape(-1).view(torch.uint8).numpy(), config, stream,
-                          _stream_chunk_size(self.chunk_size, config.element_size), modes))
-        codebooks = tuple(book for book in self.export_codebooks() if book.codebook_id in used)
-        prefix, codebook_metadata = _pack_codebooks(codebooks)
-        packed, groups = huff0.compress_direct_storage(
-            specs, prefix, min_saving_bytes=self.min_saving_bytes, threads=self.threads,
-            compression_threshold=self.compression_threshold)
-        return pack_direct_storage(named_tensors, specs, codebooks, prefix, codebook_metadata, packed, groups)
-
-    def _add_global_codebooks(self):
-        # Global per-dtype codebooks ship as files next to the package in the
-        # reference (compressor.py:83-99); none are bundled there or here.
-        next_id = max((book.codebook_id for book in self._codebook_payloads), default=-1) + 1
-        for config in DTYPES.values():
-            for stream_id, filename in config.global_codebooks:
-                key = config.name, stream_id
-                path = Path(__file__).with_name("codebooks") / filename
-                if key in self._global_modes or not path.is_file():
-                    continue
-                header = path.read_bytes()
-                self._codebook_payloads.append(CodebookPayload(next_id, stream_id, config.name, codebook=header))
-                self._global_modes[key] = {"kind": "shared_huff0", "codebook_id": next_id,
-                                           "codebook": huff0.build_codebook_from_header(header)}
-                next_id += 1
-
-    def export_codebooks(self):
-        return tuple(self._codebook_payloads)
-
-    def load_codebooks(self, codebooks):
-        """Own copies of small tables; keep decode tables whose contents match."""
-        payloads = {book.codebook_id: replace(book, codebook=bytes(book.codebook), vocab=bytes(book.vocab))
-                    for book in codebooks}
-        previous = getattr(self, "_codebook_payload_by_id", {})
-        self._decode_codebooks = {key: table for key, table in getattr(self, "_decode_codebooks", {}).items()
-                                  if previous.get(key) == payloads.get(key)}
-        self._codebook_payload_by_id = payloads
-
+    # ------------------------------------------------------------ transfer plan
     @staticmethod
     def _transfer_plan_key(name, tensor, stream_id):
         return str(name), DTYPES[tensor.dtype].name, int(stream_id)
 
+    def _lane_plan(self, name, spec, lane, numel):
+        n_chunks = -(-numel // _stream_chunk_size(self.chunk_size, spec.element_size))
+        for source in (name, *_PLAN_ALIASES.get(name, ())):
+            key = (source, spec.name, lane)
+            if key in self._setup.tensor_codebooks:
+                fallback = self._setup.tensor_codebooks[key]
+                fallback = -1 if fallback is None else int(fallback)
+                assigned = self._setup.chunk_codebooks.get((*key, numel))
+                if assigned is None:
+                    return _LanePlan(fallback, np.full(n_chunks, fallback, dtype=np.int64))
+                ids = np.array([-1 if i is None else int(i) for i in assigned], dtype=np.int64)
+                return _LanePlan(fallback, ids)
+        fallback = self._globals.get((spec.name, lane))
+        fallback = -1 if fallback is None else int(fallback)
+        return _LanePlan(fallback, np.full(n_chunks, fallback, dtype=np.int64))
+
     def prepare_storage_transfer_target(self, named_tensors):
-        """Per (tensor, stream): the parent mode and one mode per chunk."""
-        parents, chunks = {}, {}
+        """Resolve the plan of every lane of every tensor."""
+        self._plans = {}
         for name, tensor in named_tensors:
-            config = DTYPES[tensor.dtype]
-            candidates = (str(name), *_TRANSFER_NAME_FALLBACKS.get(str(name), ()))
-            step = _stream_chunk_size(self.chunk_size, config.element_size)
-            count = (tensor.numel() + step - 1) // step
-            for stream in config.stream_ids:
-                target = self._transfer_plan_key(name, tensor, stream)
-                source = next(((c, config.name, stream) for c in candidates
-                               if (c, config.name, stream) in self._mode_by_tensor_stream), None)
-                parent = self._mode_by_tensor_stream.get(
-                    source, self._global_modes.get((config.name, stream), {"kind": "raw"}))
-                parents[target] = parent
-                exact = (*source, tensor.numel()) if source is not None else None
-                chunks[target] = self._chunk_modes.get(exact, (parent,) * count)
-        self._transfer_mode_by_tensor_stream = parents
-        self._transfer_chunk_modes = chunks
+            spec = DTYPES[tensor.dtype]
+            for lane in spec.stream_ids:
+                self._plans[(str(name), spec.name, lane)] = self._lane_plan(str(name), spec, lane, tensor.numel())
+        return self
 
     def prepare_gpu_transfer_target(self, named_tensors):
-        self.prepare_storage_transfer_target(named_tensors)
+        return self.prepare_storage_transfer_target(named_tensors)
 
-    def _mode_for_tensor_stream(self, name, tensor, stream_id):
-        return self._transfer_mode_by_tensor_stream[self._transfer_plan_key(name, tensor, stream_id)]
+    def chunk_codebook_ids(self, name, tensor, stream_id=None):
+        """Codebook id per chunk (-1: raw) of a tensor's lane in the prepared
+        plan (by default the dtype's selected lane)."""
+        spec = DTYPES[tensor.dtype]
+        lane = spec.selected_stream if stream_id is None else int(stream_id)
+        return self._plans[(str(name), spec.name, lane)].chunks
 
-    def _native_decode_spec(self, tensor):
-        config = DTYPES[getattr(torch, tensor.dtype)]
-        groups = []
-        for group in tensor.groups:
+    def export_codebooks(self):
+        return tuple(self._payloads[i] for i in sorted(self._payloads))
+
+    def codebook(self, codebook_id):
+        """The payload of a codebook id."""
+        return self._payloads[int(codebook_id)]
+
+    def _load_global_codebooks(self):
+        """Per-dtype global codes shipped as files next to the package
+        (DTypeSpec.global_codebooks; none are bundled), numbered after the
+        setup's own."""
+        folder = Path(__file__).with_name("codebooks")
+        next_id = max(self._payloads, default=-1) + 1
+        for spec in DTYPES.values():
+            for lane, filename in spec.global_codebooks:
+                path = folder / filename
+                if (spec.name, lane) in self._globals or not path.is_file():
+                    continue
+                self._payloads[next_id] = CodebookPayload(next_id, lane, spec.name, codebook=path.read_bytes())
+                self._globals[(spec.name, lane)] = next_id
+                next_id += 1
+
+    def _encoder(self, codebook_id):
+        table = self._encoders.get(codebook_id)
+        if table is None:
+            book = self._payloads[codebook_id]
+            table = self._encoders[codebook_id] = huff0.build_codebook_from_header(book.codebook, vocab=book.vocab)
+        return table
+
+    # ------------------------------------------------------------ encode
+    def encode(self, named_tensors):
+        """(blob tensor, metadata, size fields, seconds) of storage v2."""
+        named = tuple(named_tensors)
+        self._load_global_codebooks()
+        self.prepare_storage_transfer_target(named)
+        (blob, metadata, sizes), seconds = time_call(self._write_storage, named)
+        return blob, metadata, sizes, seconds
+
+    def _write_storage(self, named):
+        specs, used = [], set()
+        for name, tensor in named:
+            spec = DTYPES[tensor.dtype]
+            lane = spec.selected_stream
+            ids = self.chunk_codebook_ids(name, tensor, lane)
+            used.update(int(i) for i in np.unique(ids) if i >= 0)
+            modes = {-1: {"kind": "raw"}}
+            for i in np.unique(ids):
+                if i >= 0:
+                    modes[int(i)] = {"kind": self._payloads[int(i)].mode, "codebook_id": int(i),
+                                     "codebook": self._encoder(int(i))}
+            specs.append((tensor_words(tensor), spec, lane, _stream_chunk_size(self.chunk_size, spec.element_size),
+                          tuple(modes[int(i)] for i in ids)))
+        books = tuple(book for book in self.export_codebooks() if book.codebook_id in used)
+        prefix, records = _pack_codebooks(books)
+        packed, groups = huff0.compress_direct_storage(
+            specs, prefix, min_saving_bytes=self.min_saving_bytes, threads=self.threads,
+            compression_threshold=self.compression_threshold)
+        return pack_direct_storage(named, specs, books, prefix, records, packed, groups)
+
+    # ------------------------------------------------------------ decode
+    def load_codebooks(self, codebooks):
+        """Make storage codebooks the ones chunks refer to by id."""
+        self._payloads = {int(book.codebook_id): book for book in codebooks}
+        self._encoders = {}
+
+    def _decoder(self, book):
+        key = (book.mode, bytes(book.codebook), bytes(book.vocab))
+        table = self._decoders.get(key)
+        if table is None:
+            table = self._decoders[key] = huff0.build_decodebook(key[1], vocab=key[2])
+        return table
+
+    def decode(self, blob, metadata):
+        """{name: CPU tensor} of a storage v2 archive, bit for bit."""
+        codebooks, tensors = unpack_storage(blob, metadata)
+        self.load_codebooks(codebooks)
+        decoded = {}
+        for batch in self._batches(tensors):
+            words = huff0.decompress_mixed_streams_many([self._decode_spec(t) for t in batch], threads=self.threads)
+            for record, data in zip(batch, words, strict=True):
+                decoded[record.name] = _tensor_from_raw_bytes(data, getattr(torch, record.dtype), record.shape)
+        return decoded
+
+    def _batches(self, tensors):
+        """Consecutive tensors with at most direct_batch_bytes of output per
+        batch (a larger tensor is a batch of its own)."""
+        batch, size = [], 0
+        for record in tensors:
+            if batch and size + record.raw_bytes > self.direct_batch_bytes:
+                yield batch
+                batch, size = [], 0
+            batch.append(record)
+            size += record.raw_bytes
+        if batch:
+            yield batch
+
+    def _decode_spec(self, record):
+        """(element size, reorder, numel, lanes) for the native decoder; each
+        lane a tuple of (mode, payload, symbols, decode table) per chunk."""
+        spec = _SPECS_BY_NAME[record.dtype]
+        lanes = []
+        for lane, group in enumerate(record.groups):
             chunks = []
             for chunk in group.chunks:
                 table = None
                 if chunk.mode != "raw":
-                    book = self._codebook_payload_by_id[chunk.codebook_id]
-                    if (book.dtype, book.stream_id, book.mode) != (tensor.dtype, len(groups), chunk.mode):
+                    book = self._payloads[chunk.codebook_id]
+                    if (book.dtype, book.stream_id, book.mode) != (record.dtype, lane, chunk.mode):
                         raise ValueError("Chunk codebook does not match its tensor stream.")
-                    if chunk.codebook_id not in self._decode_codebooks:
-                        self._decode_codebooks[chunk.codebook_id] = huff0.build_decodebook(book.codebook,
-                                                                                           vocab=book.vocab)
-                    table = self._decode_codebooks[chunk.codebook_id]
+                    table = self._decoder(book)
                 chunks.append((chunk.mode, chunk.payload, chunk.symbol_count, table))
-            groups.append(tuple(chunks))
-        return config.element_size, bool(config.bit_reorder), tensor.numel, tuple(groups)
-
-    def _decompress_tensors(self, payloads):
-        outputs, batch, batch_bytes = [], [], 0
-
-        def flush():
-            nonlocal batch_bytes
-            raw = huff0.decompress_mixed_streams_many(tuple(self._native_decode_spec(t) for t in batch),
-                                                      threads=self.threads)
-            outputs.extend(_tensor_from_raw_bytes(data, getattr(torch, t.dtype), t.shape)
-                           for t, data in zip(batch, raw, strict=True))
-            batch.clear()
-            batch_bytes = 0
-
-        for tensor in payloads:
-            if batch and batch_bytes + tensor.raw_bytes > self.direct_batch_bytes:
-                flush()
-            batch.append(tensor)
-            batch_bytes += tensor.raw_bytes
-        if batch:
-            flush()
-        return tuple(outputs)
+            lanes.append(tuple(chunks))
+        return spec.element_size, bool(spec.bit_reorder), record.numel, tuple(lanes)

@@ -56,6 +56,26 @@ void restore(const uint8_t* const* lanes, uint64_t length, unsigned es, bool reo
 
 constexpr size_t kSharedMetadata = 25;   // direct_storage.h:1, payloads.py:5-11
 
+// The stored form of one chunk of the selected lane (direct_storage.h:
+// 160-177): the codebook's block when it is at most the chunk's budget
+// (threshold x length minus the 25 metadata bytes of a coded chunk) and also
+// saves min_saving_bytes, else the raw bytes. Writes the block into dst
+// (capacity: the chunk's length) and returns its size, or 0 for raw.
+size_t coded_chunk(int mode, const nz_codebook* book, const uint8_t* symbols, uint64_t length, uint8_t* dst,
+                   uint64_t min_saving_bytes, double threshold) {
+    const int64_t budget = static_cast<int64_t>(length * threshold) - static_cast<int64_t>(kSharedMetadata);
+    size_t size = 0;
+    if (budget > 0 && mode == 1) {
+        // codebooks.h:114-142: stream capacity = chunk length, result <= budget
+        size = nz::huff0_encode4x(book->huff, symbols, length, dst, length);
+        if (size > static_cast<uint64_t>(budget)) size = 0;
+    } else if (budget > 0 && mode == 2) {
+        size = nz::nzm1_encode(book->book, symbols, length, dst, static_cast<size_t>(budget));
+    }
+    if (size && size + min_saving_bytes < length && size + kSharedMetadata < length * threshold) return size;
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -104,6 +124,22 @@ int nz_count_mixed_tokens(const uint8_t* data, size_t size, const uint8_t* vocab
             ++counts[pair ? pair : data[i]];
             i += pair ? 2 : 1;
         }
+    });
+}
+
+int nz_storage_chunk_size(const nz_codebook* book, int mode, const uint8_t* symbols, size_t length,
+                          uint64_t min_saving_bytes, double threshold, int32_t* stored_mode, uint64_t* stored_bytes) {
+    return nz_capi::guarded([&] {
+        if (!stored_mode || !stored_bytes || (length && !symbols)) nz::fail(nz::kInvalidArgument, "Null size argument.");
+        if (mode < 0 || mode > 2) nz::fail(nz::kInvalidArgument, "Unsupported chunk encoding mode.");
+        if (mode && (!book || book->book.mixed != (mode == 2)))
+            nz::fail(nz::kInvalidArgument, "Codebook format does not match chunk mode.");
+        if (!(threshold > 0 && threshold <= 1)) nz::fail(nz::kInvalidArgument, "compression_threshold must be in (0, 1].");
+        std::vector<uint8_t> scratch(length + 16);
+        const size_t size = mode ? coded_chunk(mode, book, symbols, length, scratch.data(), min_saving_bytes, threshold)
+                                 : 0;
+        *stored_mode = size ? mode : 0;
+        *stored_bytes = size ? size : length;
     });
 }
 
@@ -173,18 +209,10 @@ int nz_storage_compress(const nz_storage_tensor* tensors, size_t count, const ui
             extract(t, job.start, job.length, out + raw_base + raw_offset[job.tensor], symbols.data());
             uint8_t* dst = out + selected_base + symbol_offset[job.tensor] + job.start;
             job.payload_size = job.length;
-            const int64_t budget = static_cast<int64_t>(job.length * threshold) - static_cast<int64_t>(kSharedMetadata);
             const int mode = t.chunk_modes[local];
-            size_t size = 0;
-            if (budget > 0 && mode == 1) {
-                // codebooks.h:114-142: stream capacity = chunk length, result <= budget
-                size = nz::huff0_encode4x(t.chunk_books[local]->huff, symbols.data(), job.length, dst, job.length);
-                if (size > static_cast<uint64_t>(budget)) size = 0;
-            } else if (budget > 0 && mode == 2) {
-                size = nz::nzm1_encode(t.chunk_books[local]->book, symbols.data(), job.length, dst,
-                                       static_cast<size_t>(budget));
-            }
-            if (size && size + min_saving_bytes < job.length && size + kSharedMetadata < job.length * threshold) {
+            const size_t size = coded_chunk(mode, t.chunk_books[local], symbols.data(), job.length, dst,
+                                            min_saving_bytes, threshold);
+            if (size) {
                 job.mode = mode;
                 job.payload_size = size;
             } else if (job.length) {

@@ -25,7 +25,7 @@ from neuralzip_amd._native import KIND_LONG, KIND_RAW
 from neuralzip_amd.compressor import NeuralZipCompressor
 from neuralzip_amd.dtypes import DTYPES, DTypeSpec
 from neuralzip_amd.gpu import decoder as gpu_decoder
-from neuralzip_amd.utils import _stream_chunk_size
+from neuralzip_amd.utils import _stream_chunk_size, tensor_words
 
 RUNTIME_ATTRIBUTE = "neuralzip_runtime"
 _GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
@@ -175,6 +175,7 @@ class NeuralZipModelExport:
     groups: tuple
     tensors: tuple = field(default=(), repr=False)   # (layout, codebook ids, offset, dtype, block name)
     codebooks: dict = field(default_factory=dict, repr=False)
+    hooks: dict = field(default_factory=dict, repr=False)   # block -> hooked module path, where they differ
 
     @cached_property
     def block_order(self):
@@ -183,6 +184,39 @@ class NeuralZipModelExport:
     @cached_property
     def bindings(self):
         return tuple(dict.fromkeys(binding for group in self.groups for binding in group.bindings))
+
+    def byte_totals(self):
+        """Byte accounting of the fragments for the GPU representation's stats.
+
+        raw / coded: the fragments' words and their device form (coded lane:
+        bitstream, window metadata and tiles; other lanes raw); selected_raw
+        / selected_coded: the same for coded lanes alone; exponent_raw /
+        exponent_coded: the exponent lanes (None when a dtype has none);
+        tables: device LUT image bytes of each codebook in use;
+        exponent_books: codebooks that code exponent lanes."""
+        totals = dict(raw=0, coded=0, selected_raw=0, selected_coded=0, exponent_raw=0, exponent_coded=0)
+        exponent_books, exponent_known, tables = set(), True, {}
+        for group in self.groups:
+            encoded, lane = group.encoded, group.encoded.dtype.exponent_stream
+            totals["raw"] += encoded.raw_bytes
+            totals["coded"] += encoded.compressed_bytes
+            if group.codebook_id not in tables:
+                tables[group.codebook_id] = 4 * len(group.codebook.decode_lut)
+            for index, stream in enumerate(encoded.streams):
+                if isinstance(stream, GPUEncodedSymbols):
+                    totals["selected_raw"] += stream.symbol_count
+                    totals["selected_coded"] += stream.compressed_bytes
+                    if index == lane:
+                        exponent_books.add(group.codebook_id)
+            if lane is None:
+                exponent_known = False
+            else:
+                stream = encoded.streams[lane]
+                totals["exponent_raw"] += encoded.numel
+                totals["exponent_coded"] += stream.compressed_bytes if isinstance(stream, GPUEncodedSymbols) else stream
+        if not exponent_known:
+            totals["exponent_raw"] = totals["exponent_coded"] = None
+        return dict(totals, tables=tables, exponent_books=exponent_books)
 
     @property
     def workspace_sizes(self):
@@ -201,66 +235,87 @@ class _Candidate:
     parameter: nn.Parameter = field(repr=False, compare=False)
 
 
-def _join(parent, child):
-    return f"{parent}.{child}" if parent and child else parent or child
+def _dotted(*parts):
+    return ".".join(part for part in parts if part)
 
 
-def _decode_hook_module(model, block_name):
-    parent_name, _, child_name = block_name.rpartition(".")
-    parent = model.get_submodule(parent_name)
-    # MultiheadAttention reads out_proj.weight without calling the child Linear
-    if child_name == "out_proj" and isinstance(parent, nn.MultiheadAttention):
-        return parent
-    return model.get_submodule(block_name)
+def _owns_linear(module):
+    """An nn.Linear reachable from `module` without entering a ModuleList:
+    a ModuleList's entries are blocks of their own."""
+    if isinstance(module, nn.Linear):
+        return True
+    if isinstance(module, nn.ModuleList):
+        return False
+    return any(_owns_linear(child) for child in module._modules.values() if child is not None)
 
 
-def _gpu_candidates(model):
-    """Blocks are ModuleList children (outermost that still owns Linear
-    layers of its own); other weight modules are their own blocks
-    (inference.py:232-274)."""
-    possible = [(_join(parent_name, child_name), child)
-                for parent_name, parent in model.named_modules(remove_duplicate=False)
-                if isinstance(parent, nn.ModuleList)
-                for child_name, child in parent._modules.items() if child is not None]
-    names = {name for name, _ in possible}
-    blocks = []
-    for name, module in possible:
-        if any(name.startswith(parent + ".") for parent, _ in blocks):
-            continue
-        nested = tuple(child + "." for child in names if child.startswith(name + "."))
-        if nested and all((_join(name, child) + ".").startswith(nested)
-                          for child, layer in module.named_modules(remove_duplicate=False)
-                          if isinstance(layer, nn.Linear)):
-            continue
-        blocks.append((name, module))
-    candidates = []
-    for module_name, module in model.named_modules(remove_duplicate=False):
-        if not isinstance(module, _GPU_WEIGHT_TYPES):
-            continue
-        parameter = module._parameters.get("weight")
-        if isinstance(parameter, nn.Parameter):
-            block = next((name for name, _ in blocks
-                          if module_name == name or module_name.startswith(name + ".")), module_name)
-            candidates.append(_Candidate(block, module_name, _join(module_name, "weight"), parameter))
-    return tuple(dict.fromkeys(c.block_name for c in candidates)), tuple(candidates)
+def _holds_entries(module):
+    """Whether `module` is, or contains, a ModuleList with at least one entry."""
+    children = [child for child in module._modules.values() if child is not None]
+    if isinstance(module, nn.ModuleList) and children:
+        return True
+    return any(_holds_entries(child) for child in children)
 
 
-def _unique_candidates(model, candidates):
-    """Drop tied/shared parameters (inference.py:277-285)."""
-    occurrences = defaultdict(int)
-    for _name, parameter in model.named_parameters(remove_duplicate=False):
-        occurrences[id(parameter)] += 1
-    return tuple(c for c in candidates if c.parameter.numel() and occurrences[id(c.parameter)] == 1)
+@dataclass
+class _ModelScan:
+    """What one walk over every module path of a model finds."""
+    candidates: list = field(default_factory=list)   # _Candidate, in walk order
+    hooks: dict = field(default_factory=dict)        # block name -> path of the module its hook goes on
+    uses: dict = field(default_factory=dict)         # id(parameter) -> module paths holding it
+
+
+def _scan_model(model):
+    """Blocks, weight candidates and parameter sharing (inference.py:219-285).
+
+    A block is an entry of a ModuleList, at the outermost level where it owns
+    an nn.Linear itself (an entry whose Linears all sit in ModuleLists below
+    it gives way to their entries); a weight module outside every block is
+    a block of its own. Weight modules are nn.Linear, nn.Conv2d and GPT-2's
+    Conv1D with a `weight` Parameter. nn.MultiheadAttention reads its
+    out_proj weight without calling the Linear, so a standalone out_proj
+    block is hooked on the attention module. Every module path is walked,
+    shared modules once per path."""
+    scan = _ModelScan()
+
+    def visit(module, path, block, parent):
+        for value in module._parameters.values():
+            if value is not None:
+                scan.uses[id(value)] = scan.uses.get(id(value), 0) + 1
+        weight = module._parameters.get("weight") if isinstance(module, _GPU_WEIGHT_TYPES) else None
+        if isinstance(weight, nn.Parameter):
+            owner = block or path
+            if owner not in scan.hooks:
+                standalone_out_proj = (block is None and isinstance(parent, nn.MultiheadAttention)
+                                       and path.rpartition(".")[2] == "out_proj")
+                scan.hooks[owner] = path.rpartition(".")[0] if standalone_out_proj else owner
+            scan.candidates.append(_Candidate(owner, path, _dotted(path, "weight"), weight))
+        for name, child in module._modules.items():
+            if child is None:
+                continue
+            child_path = _dotted(path, name)
+            child_block = block
+            if block is None and isinstance(module, nn.ModuleList) and (
+                    _owns_linear(child) or not _holds_entries(child)):
+                child_block = child_path
+            visit(child, child_path, child_block, module)
+
+    visit(model, "", None, None)
+    return scan
+
+
+def _hook_module(model, exported, block_name):
+    return model.get_submodule(exported.hooks.get(block_name, block_name))
 
 
 def _align(value, alignment=WORKSPACE_ALIGNMENT):
     return (value + alignment - 1) // alignment * alignment
 
 
-def _assemble_export(block_order, candidates, compressor, threads=0):
-    """Encode every candidate's chunks; keep a tensor only if its fragments
-    are smaller than its raw bytes (inference.py:288-336)."""
-    payloads = {int(p.codebook_id): p for p in compressor.export_codebooks()}
+def _assemble_export(block_order, candidates, compressor, threads=0, hooks=None):
+    """Encode every candidate's chunks with the codebooks of the transfer
+    plan; keep a tensor only if its fragments are smaller than its raw
+    bytes (inference.py:288-336)."""
     codebooks = {}
     block_index = {name: i for i, name in enumerate(block_order)}
     offsets = defaultdict(int)
@@ -268,21 +323,16 @@ def _assemble_export(block_order, candidates, compressor, threads=0):
     for member in sorted(candidates, key=lambda c: (block_index[c.block_name], c.module_name)):
         parameter = member.parameter
         config = DTYPES[parameter.dtype]
-        stream_id = config.selected_stream
-        modes = compressor._transfer_chunk_modes[compressor._transfer_plan_key(member.tensor_name, parameter,
-                                                                               stream_id)]
+        ids = compressor.chunk_codebook_ids(member.tensor_name, parameter)
         step = _stream_chunk_size(compressor.chunk_size, config.element_size)
-        raw = parameter.detach().cpu().contiguous().reshape(-1).view(torch.uint8).numpy()
-        ids, fragments = [], []
-        for chunk, mode in enumerate(modes):
-            codebook_id = int(mode.get("codebook_id", -1)) if mode["kind"] != "raw" else -1
+        raw = tensor_words(parameter)
+        fragments = []
+        for chunk, codebook_id in enumerate(ids.tolist()):
             if codebook_id != -1 and codebook_id not in codebooks:
-                codebooks[codebook_id] = GPUCodebook.from_payload(payloads[codebook_id])
+                codebooks[codebook_id] = GPUCodebook.from_payload(compressor.codebook(codebook_id))
             start = chunk * step
             part = raw[start * config.element_size:(start + step) * config.element_size]
-            book = codebooks[codebook_id].native if codebook_id != -1 else None
-            fragments.append((part, book, start, config))
-            ids.append(codebook_id)
+            fragments.append((part, codebooks[codebook_id].native if codebook_id != -1 else None, start, config))
         layout = _native.Layout(fragments, threads=threads)
         encoded = [_fragment(layout, i, config, len(f[0]) // config.element_size) for i, f in enumerate(fragments)]
         if sum(e.compressed_bytes for e in encoded) >= raw.size:
@@ -291,26 +341,30 @@ def _assemble_export(block_order, candidates, compressor, threads=0):
         workspace_offset = offsets[key]
         binding = LinearWeightBinding(member.module_name, member.tensor_name, tuple(parameter.shape),
                                       parameter.numel(), workspace_offset)
-        for chunk, (codebook_id, enc) in enumerate(zip(ids, encoded)):
+        for chunk, (codebook_id, enc) in enumerate(zip(ids.tolist(), encoded)):
             groups.append(GPUWeightGroup(member.block_name, codebook_id,
                                          codebooks[codebook_id] if codebook_id != -1 else GPUCodebook((), ()),
                                          enc, (binding,), workspace_offset + chunk * step))
-        tensors.append((layout, tuple(ids), workspace_offset, config, member.block_name))
+        tensors.append((layout, tuple(ids.tolist()), workspace_offset, config, member.block_name))
         offsets[key] = _align(workspace_offset + parameter.numel())
-    return NeuralZipModelExport(tuple(groups), tuple(tensors), codebooks)
+    used = {g.block_name for g in groups}
+    hooks = {name: path for name, path in (hooks or {}).items() if name in used and path != name}
+    return NeuralZipModelExport(tuple(groups), tuple(tensors), codebooks, hooks)
 
 
 def export_model_for_gpu(model, setup, *, allowed_dtypes=DTYPES, threads=0):
     """Export the frozen chunk tables, including adaptive singleton/pair codes."""
-    blocks, candidates = _gpu_candidates(model)
-    candidates = tuple(c for c in _unique_candidates(model, candidates)
-                       if c.parameter.dtype in DTYPES and c.parameter.dtype in allowed_dtypes
+    scan = _scan_model(model)
+    block_order = tuple(dict.fromkeys(c.block_name for c in scan.candidates))
+    candidates = tuple(c for c in scan.candidates
+                       if c.parameter.numel() and scan.uses[id(c.parameter)] == 1
+                       and c.parameter.dtype in DTYPES and c.parameter.dtype in allowed_dtypes
                        and c.parameter.is_contiguous())
     if not candidates:
         return NeuralZipModelExport(())
     compressor = NeuralZipCompressor(setup, gpu=True)
     compressor.prepare_gpu_transfer_target(tuple((c.tensor_name, c.parameter) for c in candidates))
-    return _assemble_export(blocks, candidates, compressor, threads=threads)
+    return _assemble_export(block_order, candidates, compressor, threads=threads, hooks=scan.hooks)
 
 
 def export_tensors_for_gpu(named_tensors, setup, *, threads=0):
@@ -547,7 +601,7 @@ class NeuralZipRuntime:
                     _binding_module(self.model, binding).__dict__["weight"] = self._binding_view(
                         group.encoded.dtype.torch_dtype, name, binding)
         for name in self.export.block_order:
-            handle = _decode_hook_module(self.model, name).register_forward_pre_hook(
+            handle = _hook_module(self.model, self.export, name).register_forward_pre_hook(
                 partial(self._decode_block, name), prepend=True, with_kwargs=True)
             self._hook_handles.append(handle)
         blocks = {b.module_name: g.block_name for g in self.export.groups for b in g.bindings}

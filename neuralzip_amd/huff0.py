@@ -59,6 +59,8 @@ def _lib():
         L.nz_storage_compress.argtypes = [vp, sz, vp, sz, u64, ctypes.c_int, ctypes.c_double, vp, sz,
                                           ctypes.POINTER(sz), vp]
         L.nz_storage_decompress.argtypes = [vp, sz, ctypes.c_int]
+        L.nz_storage_chunk_size.argtypes = [vp, ctypes.c_int, vp, sz, u64, ctypes.c_double,
+                                            ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(u64)]
         L._storage_bound = True
     return L
 
@@ -173,6 +175,18 @@ def decode_block(book, payload, symbols):
     _native.check(_lib().nz_codebook_decode_block(_book_pointer(book), _addr(src), src.size, out.ctypes.data,
                                                   symbols))
     return out[:symbols].tobytes()
+
+
+def stored_chunk_size(book, mode, symbols, *, min_saving_bytes=0, compression_threshold=0.95):
+    """(stored mode, payload bytes) of one selected-lane chunk under the
+    storage encoder's raw-fallback rule (nz_storage_chunk_size)."""
+    data = _array(symbols)
+    stored, size = ctypes.c_int32(), ctypes.c_uint64()
+    _native.check(_lib().nz_storage_chunk_size(_book_pointer(book) if book is not None else None, _MODE_IDS[mode],
+                                               _addr(data), data.size, int(min_saving_bytes),
+                                               float(compression_threshold), ctypes.byref(stored),
+                                               ctypes.byref(size)))
+    return _MODE_NAMES[stored.value], size.value
 
 
 def compress_direct_storage(tensor_specs, prefix, *, min_saving_bytes=0, threads=0, compression_threshold=0.95):

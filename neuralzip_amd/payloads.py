@@ -1,24 +1,55 @@
-"""Payload records and size accounting (neuralzip/payloads.py:1-174).
+"""Payload records and the canonical size accounting of storage v2
+(neuralzip/payloads.py).
 
-Field names and the canonical byte accounting follow the reference so that
-stats, setups and storage metadata read the same.
+The record classes and their field names are an interface: setup pickles
+hold CodebookPayload objects, and NeuralZipStats is `model.neuralzip_stats`.
+
+Stats count the blob plus the bytes its metadata would take in a compact
+binary encoding (not the JSON text the checkpoint holds), derived here from
+one schema: integers take their width, text a u32 length and its UTF-8
+bytes, byte fields a u64 length and their bytes.
 """
 from dataclasses import dataclass
 
 from neuralzip_amd.dtypes import DTYPES
 
-RAW_CHUNK_METADATA_BYTES = 17
-SHARED_CHUNK_METADATA_BYTES = 25
+_U8, _U16, _U32, _U64 = 1, 2, 4, 8
+
+
+def _text(value):
+    return _U32 + len(str(value).encode("utf-8"))
+
+
+def _blob(value):
+    return _U64 + len(value)
+
+
+# A chunk record: mode byte, symbol count, payload size, and the codebook id
+# when the chunk is coded.
+RAW_CHUNK_METADATA_BYTES = _U8 + _U64 + _U64
+SHARED_CHUNK_METADATA_BYTES = RAW_CHUNK_METADATA_BYTES + _U64
 CHUNK_METADATA_BYTES = {
     "raw": RAW_CHUNK_METADATA_BYTES,
     "shared_huff0": SHARED_CHUNK_METADATA_BYTES,
     "mixed_huffman": SHARED_CHUNK_METADATA_BYTES,
 }
+# Archive header: magic, version, format name, codebook and tensor counts.
+_HEADER_BYTES = _U32 + _U16 + _text("neuralzip") + _U64 + _U64
+
+
+def codebook_metadata_bytes(dtype, mode, codebook, vocab):
+    """A codebook record: id, lane, dtype, mode, header bytes, vocabulary bytes."""
+    return _U64 + _U32 + _text(dtype) + _text(mode) + _blob(codebook) + _blob(vocab)
+
+
+def _tensor_record_bytes(name, dtype, shape):
+    """Name, dtype, element size, element count, reorder flag, the shape and
+    the number of lanes; the lanes' chunk lists follow."""
+    return _text(name) + _text(dtype) + 3 * _U64 + _U64 * len(shape) + _U64
 
 
 @dataclass(frozen=True)
 class NeuralZipStats:
-    """`model.neuralzip_stats` (payloads.py:14-50)."""
     setup_seconds: float
     encoding_seconds: float
     raw_bytes: int
@@ -53,14 +84,6 @@ class NeuralZipStats:
         return self.setup_seconds + self.encoding_seconds
 
 
-def _bytes_field(value):
-    return 8 + len(value)
-
-
-def _text_field(value):
-    return 4 + len(str(value).encode("utf-8"))
-
-
 @dataclass(frozen=True)
 class CodebookPayload:
     codebook_id: int
@@ -72,7 +95,7 @@ class CodebookPayload:
 
     @property
     def metadata_bytes(self):
-        return codebook_metadata_bytes(self)
+        return codebook_metadata_bytes(self.dtype, self.mode, self.codebook, self.vocab)
 
 
 @dataclass(frozen=True)
@@ -115,40 +138,35 @@ class TensorPayload:
         return self.numel * self.element_size
 
 
-def codebook_metadata_bytes(codebook):
-    """id (8) + stream (4) + dtype and mode texts + the two byte fields."""
-    return (8 + 4 + _text_field(codebook.dtype) + _text_field(codebook.mode)
-            + _bytes_field(codebook.codebook) + _bytes_field(codebook.vocab))
-
-
 def storage_bytes(codebooks, tensors, blob_bytes):
-    """Blob plus canonical metadata bytes (payloads.py:127-174)."""
+    """Size fields of NeuralZipStats for a storage archive: `tensors` are the
+    metadata's tensor records. Compressed = blob + metadata records (the
+    codebook payloads themselves are in the blob); the exponent figures
+    cover the exponent lanes, their chunk records and the codebooks of
+    those lanes, and are None when a non-empty tensor has no exponent lane."""
     specs = {spec.name: spec for spec in DTYPES.values()}
-    raw_bytes = exponent_raw = exponent_compressed = 0
-    exponent_defined = True
-    exponent_streams = set()
-    structural = 4 + 2 + _text_field("neuralzip") + 8 + 8
-    structural += sum(book.metadata_bytes - len(book.codebook) - len(book.vocab) for book in codebooks)
-    for tensor in tensors:
-        spec = specs[tensor["dtype"]]
-        numel = tensor["numel"]
-        raw_bytes += numel * tensor["element_size"]
-        if numel and spec.exponent_stream is None:
-            exponent_defined = False
-        if spec.exponent_stream is not None:
-            exponent_raw += numel
-            exponent_streams.add((spec.name, spec.exponent_stream))
-        structural += _text_field(tensor["name"]) + _text_field(tensor["dtype"]) + 24 + 8 * len(tensor["shape"]) + 8
-        for stream, group in enumerate(tensor["groups"]):
-            chunk_meta = sum(CHUNK_METADATA_BYTES[chunk["mode"]] for chunk in group)
-            structural += 8 + chunk_meta
-            if stream == spec.exponent_stream:
-                exponent_compressed += chunk_meta + sum(chunk["payload"][1] for chunk in group)
-    exponent_compressed += sum(book.metadata_bytes for book in codebooks
-                               if (book.dtype, book.stream_id) in exponent_streams)
+    metadata = _HEADER_BYTES + sum(book.metadata_bytes - len(book.codebook) - len(book.vocab) for book in codebooks)
+    raw = exponent_raw = exponent_coded = 0
+    exponent_lanes, exponent_defined = set(), True
+    for record in tensors:
+        spec = specs[record["dtype"]]
+        lane_of_exponent = spec.exponent_stream
+        raw += record["numel"] * record["element_size"]
+        metadata += _tensor_record_bytes(record["name"], record["dtype"], record["shape"])
+        if lane_of_exponent is None:
+            exponent_defined = exponent_defined and not record["numel"]
+        else:
+            exponent_raw += record["numel"]
+            exponent_lanes.add((spec.name, lane_of_exponent))
+        for lane, chunks in enumerate(record["groups"]):
+            chunk_records = sum(CHUNK_METADATA_BYTES[chunk["mode"]] for chunk in chunks)
+            metadata += _U64 + chunk_records
+            if lane == lane_of_exponent:
+                exponent_coded += chunk_records + sum(chunk["payload"][1] for chunk in chunks)
+    exponent_coded += sum(book.metadata_bytes for book in codebooks if (book.dtype, book.stream_id) in exponent_lanes)
     return {
-        "raw_bytes": int(raw_bytes),
-        "compressed_bytes": int(blob_bytes + structural),
+        "raw_bytes": int(raw),
+        "compressed_bytes": int(blob_bytes + metadata),
         "exponent_raw_bytes": int(exponent_raw) if exponent_defined else None,
-        "exponent_compressed_bytes": int(exponent_compressed) if exponent_defined else None,
+        "exponent_compressed_bytes": int(exponent_coded) if exponent_defined else None,
     }

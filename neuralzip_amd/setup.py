@@ -1,25 +1,45 @@
-"""NeuralZipSetup: chunk clustering and codebook selection (neuralzip/setup.py).
+"""NeuralZipSetup: chunk clusters and their codebooks (neuralzip/setup.py).
 
-`build(model)` groups every chunk of every floating tensor by the
-Jensen-Shannon distance of its exponent histogram to the running cluster
-centroids, then gives each cluster a singleton Huff0 code or, for dtypes
-with a pure exponent lane, an NZM1 pair/singleton code when that encodes the
-cluster's samples smaller. Setups pickle (protocol 5) with the reference's
-attribute names.
+`build(model)` runs in two phases.
+
+Survey. Every non-empty floating tensor, in name order, is cut into chunks
+of `chunk_size` bytes of words. The native library histograms each chunk's
+exponent field in place and assigns the chunks, in order, to Jensen-Shannon
+clusters (`_native.Clusterer`: a chunk joins the nearest centroid of its
+dtype and forced label, or starts a cluster when it lies farther than
+`cluster_js_threshold`). A cluster keeps the selected-lane bytes of its
+first chunks, up to `max_codebook_sample_bytes`, as samples; every tensor
+keeps the byte counts of its whole selected lane.
+
+Codebooks. A cluster is coded with a singleton Huff0 code of its samples'
+byte counts or, for dtypes whose selected lane is a pure exponent lane,
+with an NZM1 code of up to 254 pair tokens (pairs whose code is longer than
+their two bytes' codes are dropped until none is) when that stores the
+samples in fewer bytes. Every tensor also gets a singleton code of its
+pooled counts, the fallback for a tensor whose chunking no longer matches.
+Identical codebooks are stored once unless shared codebooks are disabled.
+
+Setups pickle (protocol 5) with the reference's class and attribute names,
+so either library reads the other's setup files.
 """
 import io
 import pickle
-from dataclasses import dataclass
+import time
+from dataclasses import dataclass, field
 from pathlib import Path
 from statistics import median
 
 import numpy as np
 
-from neuralzip_amd import huff0
+from neuralzip_amd import _native, huff0
 from neuralzip_amd.dtypes import DTYPES
-from neuralzip_amd.payloads import CHUNK_METADATA_BYTES, CodebookPayload
-from neuralzip_amd.utils import (_floating_tensors, _model_tensors, _stream_chunk_size, _tensor_raw_bytes,
-                                 jensen_shannon_distance, time_call)
+from neuralzip_amd.payloads import CHUNK_METADATA_BYTES, CodebookPayload, codebook_metadata_bytes
+from neuralzip_amd.utils import _floating_tensors, _model_tensors, _stream_chunk_size, tensor_words
+
+_SPECS = {spec.name: spec for spec in DTYPES.values()}
+_KIND = {name: i for i, name in enumerate(_SPECS)}   # clusters never mix dtypes
+_MAX_PAIRS = 254          # NZM1 pair tokens 256..509
+_COMPARED_SAMPLES = 4     # samples encoded to choose between the two codes
 
 
 @dataclass(frozen=True)
@@ -50,12 +70,197 @@ class _SetupUnpickler(pickle.Unpickler):
         raise pickle.UnpicklingError(f"Setup pickles may not reference {module}.{name}.")
 
 
+@dataclass(eq=False)
+class _Cluster:
+    """Chunks of one dtype and forced label grouped by the survey."""
+    dtype: str
+    stream: int
+    label: object
+    weight: int = 0                       # elements of all its chunks
+    samples: list = field(default_factory=list)
+    sampled: int = 0
+
+
+class _Survey:
+    """Feeds tensors, in order, through the native clusterer and collects
+    what the codebook phase needs."""
+
+    def __init__(self, setup):
+        self.setup = setup
+        self.engine = _native.Clusterer(setup.cluster_js_threshold, setup.enable_shared_codebooks)
+        self.labels = []                  # forced labels, by native label id
+        self.clusters = []                # in the engine's numbering
+        self.chunk_clusters = {}          # (name, dtype, lane, numel) -> cluster per chunk
+        self.lane_counts = {}             # (name, dtype, lane) -> counts of the selected lane
+
+    def _label_ids(self, name, n_chunks):
+        """Native id of each chunk's forced label (-1: none): a
+        (name, chunk index) entry of cluster_map, else a name entry."""
+        rules = self.setup.cluster_map
+        if not rules:
+            return np.full(n_chunks, -1, dtype=np.int64)
+        default = rules.get(name)
+        return np.array([self._label_id(rules.get((name, i), default)) for i in range(n_chunks)], dtype=np.int64)
+
+    def _label_id(self, label):
+        if label is None:
+            return -1
+        for i, known in enumerate(self.labels):
+            if known == label:
+                return i
+        self.labels.append(label)
+        return len(self.labels) - 1
+
+    def add(self, name, tensor):
+        spec = DTYPES[tensor.dtype]
+        lane = spec.selected_stream
+        words = tensor_words(tensor)
+        step = _stream_chunk_size(self.setup.chunk_size, spec.element_size)
+        histograms, lane_counts = _native.chunk_histograms(words, spec, step)
+        n = len(histograms)
+        numel = tensor.numel()
+        lengths = np.full(n, step, dtype=np.uint64)
+        lengths[-1] = numel - step * (n - 1)
+        labels = self._label_ids(name, n)
+        assigned = self.engine.assign(histograms, _KIND[spec.name], labels, lengths)
+        budget = self.setup.max_codebook_sample_bytes
+        es = spec.element_size
+        for i, (c, length) in enumerate(zip(assigned.tolist(), lengths.tolist())):
+            if c == len(self.clusters):   # the engine numbers new clusters in order
+                self.clusters.append(_Cluster(spec.name, lane, None if labels[i] < 0 else self.labels[labels[i]]))
+            cluster = self.clusters[c]
+            cluster.weight += length
+            take = min(budget - cluster.sampled, length)
+            if take > 0:
+                first = i * step
+                sample = spec.selected_lane(words[first * es:(first + take) * es]).tobytes()
+                cluster.samples.append(sample)
+                cluster.sampled += take
+        self.chunk_clusters[(name, spec.name, lane, numel)] = tuple(assigned.tolist())
+        self.lane_counts[(name, spec.name, lane)] = lane_counts
+
+
+class _CodebookTable:
+    """The setup's codebook payloads, numbered in order of first use."""
+
+    def __init__(self, dedupe):
+        self.payloads = []
+        self._dedupe = dedupe
+        self._ids = {}
+
+    def add(self, book, dtype, lane, vocab=b""):
+        if book is None:
+            return None
+        mode = "mixed_huffman" if vocab else "shared_huff0"
+        key = (dtype, lane, mode, book.codebook, vocab) if self._dedupe else len(self.payloads)
+        if key not in self._ids:
+            self._ids[key] = len(self.payloads)
+            self.payloads.append(CodebookPayload(len(self.payloads), lane, dtype, mode, book.codebook, vocab=vocab))
+        return self._ids[key]
+
+
+def _pair_counts(samples):
+    """Counts of every adjacent byte pair (first | second << 8) inside each sample."""
+    counts = np.zeros(1 << 16, dtype=np.int64)
+    for sample in samples:
+        lane = np.frombuffer(sample, dtype=np.uint8).astype(np.uint16)
+        if lane.size > 1:
+            counts += np.bincount(lane[:-1] | (lane[1:] << 8), minlength=1 << 16)
+    return counts
+
+
+def _leading_pairs(samples, limit=_MAX_PAIRS):
+    """The `limit` most frequent pairs (ties: the smaller pair value first),
+    in ascending pair order, as NZM1 vocabularies list them."""
+    counts = _pair_counts(samples)
+    seen = np.flatnonzero(counts)
+    ranked = seen[np.lexsort((seen, -counts[seen]))]
+    return np.sort(ranked[:limit]).astype(np.uint16)
+
+
+class _CodeChooser:
+    """Singleton or pair code for each cluster (setup.py:143-249)."""
+
+    def __init__(self, setup):
+        self.setup = setup
+        self.enabled = setup.enable_shared_codebooks or setup.enable_packed_codebooks
+
+    def singleton(self, counts):
+        """Huff0 code (<= 12 bits) of 256 byte counts plus the prior; None
+        when coding is disabled or no Huff0 description exists."""
+        if not self.enabled:
+            return None
+        try:
+            return huff0.build_codebook_from_counts(counts, prior_count=self.setup.prior_count, max_bits=12)
+        except RuntimeError:
+            return None
+
+    def for_cluster(self, cluster):
+        """(codebook, pair vocabulary, report entry or None)."""
+        if not self.enabled:
+            return None, b"", None
+        spec = _SPECS[cluster.dtype]
+        concatenated = np.frombuffer(b"".join(cluster.samples), dtype=np.uint8)
+        single = self.singleton(np.bincount(concatenated, minlength=256))
+        if not self.setup.enable_packed_codebooks or spec.exponent_stream is None:
+            return single, b"", None
+        pairs = _leading_pairs(cluster.samples)
+        offered = len(pairs)
+        while len(pairs):
+            vocab = pairs.astype("<u2").tobytes()
+            counts = huff0.count_mixed_tokens(cluster.samples, vocab)
+            mixed = huff0.build_mixed_codebook(counts, vocab, prior_count=self.setup.prior_count)
+            length = np.frombuffer(mixed.codebook, dtype=np.uint8, offset=4).astype(np.int32)
+            worth = length[256:] <= length[pairs & 0xFF] + length[pairs >> 8]
+            if worth.all():
+                break
+            pairs = pairs[worth]
+        else:
+            return single, b"", None
+        report = self._compare(cluster, single, mixed, vocab)
+        report.update(candidate_pairs=offered, kept_pairs=len(pairs))
+        if report["mode"] == "mixed_huffman":
+            return mixed, vocab, report
+        return single, b"", report
+
+    def _compare(self, cluster, single, mixed, vocab):
+        """Stored bytes of up to four samples spread over the cluster's, with
+        each code under the storage encoder's raw-fallback rule, scaled to the
+        cluster's elements, plus the codebook's metadata when any sample used
+        it (setup.py:207-249); and the median time to encode them."""
+        picks = np.linspace(0, len(cluster.samples) - 1, min(_COMPARED_SAMPLES, len(cluster.samples)), dtype=int)
+        chosen = [cluster.samples[i] for i in picks]
+        sampled = sum(len(s) for s in chosen)
+        first_mode = "shared_huff0" if single is not None else "raw"
+        options = ((first_mode, single, b""), ("mixed_huffman", mixed, vocab))
+        stored, seconds = [0, 0], [[], []]
+        for repeat in range(4):   # the first pass warms up; the order alternates
+            for k in ((0, 1) if repeat % 2 == 0 else (1, 0)):
+                mode, book, vocabulary = options[k]
+                began = time.perf_counter()
+                sizes = [huff0.stored_chunk_size(book, mode, s, min_saving_bytes=self.setup.min_saving_bytes,
+                                                 compression_threshold=self.setup.compression_threshold)
+                         for s in chosen]
+                if repeat:
+                    seconds[k].append(time.perf_counter() - began)
+                coded = any(m != "raw" for m, _ in sizes)
+                total = sum(size + CHUNK_METADATA_BYTES[m] for m, size in sizes)
+                overhead = 0
+                if book is not None and coded:
+                    overhead = codebook_metadata_bytes(cluster.dtype, mode, book.codebook, vocabulary)
+                stored[k] = total * cluster.weight / sampled + overhead
+        mode = "mixed_huffman" if stored[1] < stored[0] else first_mode
+        return {"mode": mode, "singleton_bytes_estimate": stored[0], "mixed_bytes_estimate": stored[1],
+                "singleton_seconds": median(seconds[0]), "mixed_seconds": median(seconds[1])}
+
+
 class NeuralZipSetup:
     def __init__(self, *, min_saving_bytes=0, chunk_size=256 << 10, compression_threshold=0.95, prior_count=1,
                  cluster_map=None, cluster_js_threshold=0.05, max_codebook_sample_bytes=8 << 20,
                  enable_shared_codebooks=True, enable_packed_codebooks=True):
         if chunk_size < 4 or max_codebook_sample_bytes < 1 or prior_count < 1:
             raise ValueError("Chunk size >= 4, sample budget >= 1, and prior >= 1 are required.")
+        # attribute names are the pickle format of setup files
         self.min_saving_bytes = int(min_saving_bytes)
         self.chunk_size = int(chunk_size)
         self.compression_threshold = float(compression_threshold)
@@ -78,183 +283,46 @@ class NeuralZipSetup:
 
     def build(self, model, *, progress=None):
         """Cluster the chunks of `model` (a module or a tensor mapping) and
-        build the cluster codebooks. `progress(done, total, name)`, when
-        given, is called after each tensor's chunks are clustered."""
-        (groups, assignments, parents), clustering = time_call(self._cluster_chunks, _model_tensors(model),
-                                                               progress)
-        (books, chunks, tensors, report), codebook_seconds = time_call(self._build_codebooks, groups,
-                                                                       assignments, parents)
-        self.codebooks = tuple(books)
-        self.chunk_codebooks = chunks
-        self.tensor_codebooks = tensors
+        build the codebooks. `progress(done, total, name)`, when given, is
+        called after each tensor has been surveyed."""
+        tensors = _floating_tensors(_model_tensors(model))
+        began = time.perf_counter()
+        survey = _Survey(self)
+        for done, (name, tensor) in enumerate(tensors, 1):
+            survey.add(name, tensor)
+            if progress is not None:
+                progress(done, len(tensors), name)
+        clustered = time.perf_counter()
+        table = _CodebookTable(dedupe=self.enable_shared_codebooks)
+        chooser = _CodeChooser(self)
+        report, cluster_ids = [], []
+        for index, cluster in enumerate(survey.clusters):
+            book, vocab, entry = chooser.for_cluster(cluster)
+            if entry is not None:
+                report.append({"cluster": index, **entry})
+            cluster_ids.append(table.add(book, cluster.dtype, cluster.stream, vocab))
+        self.chunk_codebooks = {key: tuple(cluster_ids[c] for c in chunks)
+                                for key, chunks in survey.chunk_clusters.items()}
+        self.tensor_codebooks = {key: table.add(chooser.singleton(counts), key[1], key[2])
+                                 for key, counts in survey.lane_counts.items()}
+        self.codebooks = tuple(table.payloads)
         self.global_codebooks = {}
         self.packing_report = tuple(report)
-        self.setup_report = NeuralZipSetupReport(clustering, codebook_seconds)
+        self.setup_report = NeuralZipSetupReport(clustered - began, time.perf_counter() - clustered)
         return self
 
     def save(self, path):
-        path = Path(path)
-        path.parent.mkdir(parents=True, exist_ok=True)
-        with path.open("wb") as handle:
-            pickle.dump(self, handle, protocol=5)
-        return path
+        target = Path(path)
+        target.parent.mkdir(parents=True, exist_ok=True)
+        target.write_bytes(pickle.dumps(self, protocol=5))
+        return target
 
     @classmethod
     def load(cls, value):
+        """A setup object as is, or the setup pickled at a path (only setup
+        and payload classes may appear in the file)."""
         if not isinstance(value, cls):
-            with Path(value).open("rb") as handle:
-                value = _SetupUnpickler(io.BytesIO(handle.read())).load()
-        if not isinstance(value, cls) or not hasattr(value, "chunk_codebooks"):
-            raise TypeError("Expected a current chunk-level NeuralZip setup.")
-        return value
-
-    # -------------------------------------------------------- clustering
-    def _cluster_chunks(self, named_tensors, progress=None):
-        """Greedy JS clustering of chunk exponent histograms (setup.py:91-141)."""
-        groups, assignments, parents = [], {}, {}
-        tensors = list(_floating_tensors(named_tensors))
-        for done, (name, tensor) in enumerate(tensors, 1):
-            spec = DTYPES[tensor.dtype]
-            raw = _tensor_raw_bytes(tensor)
-            stream_id = spec.selected_stream
-            stream = spec.selected_lane(raw)
-            # with the reorder, the selected lane is the exponent field itself
-            exponents = stream if spec.bit_reorder else spec.extract_exponents(raw)
-            step = _stream_chunk_size(self.chunk_size, spec.element_size)
-            key = (str(name), spec.name, stream_id)
-            parents[key] = np.bincount(stream, minlength=256).astype(np.uint64)
-            ids = []
-            for index, start in enumerate(range(0, len(stream), step)):
-                part = stream[start:start + step]
-                counts = np.bincount(exponents[start:start + step], minlength=256)
-                distribution = counts / counts.sum()
-                forced = self.cluster_map.get((name, index), self.cluster_map.get(name))
-                compatible = [i for i, g in enumerate(groups) if g["dtype"] == spec.name and g["forced"] == forced] \
-                    if self.enable_shared_codebooks else []
-                distance, nearest = min(((jensen_shannon_distance(distribution, groups[i]["centroid"]), i)
-                                         for i in compatible), default=(float("inf"), None))
-                if nearest is None or (forced is None and distance > self.cluster_js_threshold):
-                    nearest = len(groups)
-                    groups.append({"dtype": spec.name, "stream": stream_id, "forced": forced,
-                                   "centroid": distribution, "weight": 0, "samples": [], "sampled": 0})
-                group = groups[nearest]
-                weight = len(part)
-                total = group["weight"] + weight
-                group["centroid"] = (group["centroid"] * group["weight"] + distribution * weight) / total
-                group["weight"] = total
-                budget = self.max_codebook_sample_bytes - group["sampled"]
-                if budget > 0:
-                    sample = part[:budget].tobytes()
-                    group["samples"].append(sample)
-                    group["sampled"] += len(sample)
-                ids.append(nearest)
-            assignments[(*key, tensor.numel())] = tuple(ids)
-            if progress is not None:
-                progress(done, len(tensors), name)
-        return groups, assignments, parents
-
-    # -------------------------------------------------------- codebooks
-    def _build_codebooks(self, groups, assignments, parents):
-        books, cache, report = [], {}, []
-
-        def add(book, dtype, stream, vocab=b""):
-            if book is None or not (self.enable_shared_codebooks or self.enable_packed_codebooks):
-                return None
-            mode = "mixed_huffman" if vocab else "shared_huff0"
-            key = (dtype, stream, mode, book.codebook, vocab)
-            if not self.enable_shared_codebooks:
-                key = (*key, len(books))
-            if key not in cache:
-                cache[key] = len(books)
-                books.append(CodebookPayload(len(books), stream, dtype, mode, book.codebook, vocab=vocab))
-            return cache[key]
-
-        specs = {spec.name: spec for spec in DTYPES.values()}
-        cluster_ids = []
-        for group in groups:
-            book, vocab, scores = self._prepare_codebook(group, specs[group["dtype"]])
-            if scores is not None:
-                report.append({"cluster": len(cluster_ids), **scores})
-            cluster_ids.append(add(book, group["dtype"], group["stream"], vocab))
-        chunks = {key: tuple(cluster_ids[i] for i in ids) for key, ids in assignments.items()}
-        # pooled per-tensor counts: shape-independent fallback codebooks
-        tensors = {key: add(self._singleton_codebook(counts), key[1], key[2]) for key, counts in parents.items()}
-        return books, chunks, tensors, report
-
-    def _singleton_codebook(self, counts):
-        if not (self.enable_shared_codebooks or self.enable_packed_codebooks):
-            return None
-        try:
-            return huff0.build_codebook_from_counts(counts, prior_count=self.prior_count, max_bits=12)
-        except RuntimeError:
-            return None   # some uniform alphabets have no Huff0 description; stay raw
-
-    def _prepare_codebook(self, group, spec):
-        """Singleton code, or an NZM1 code with up to 254 pairs (setup.py:178-205)."""
-        if not (self.enable_shared_codebooks or self.enable_packed_codebooks):
-            return None, b"", None
-        samples = group["samples"]
-        singleton = self._singleton_codebook(huff0.count_mixed_tokens(samples, b""))
-        if not self.enable_packed_codebooks or spec.exponent_stream is None:
-            return singleton, b"", None
-        pairs = np.zeros(65536, dtype=np.int64)
-        for sample in samples:
-            values = np.frombuffer(sample, dtype=np.uint8).astype(np.uint16)
-            pairs += np.bincount(values[:-1] | (values[1:] << 8), minlength=65536)
-        observed = np.flatnonzero(pairs)
-        ranked = np.argsort(-pairs[observed], kind="stable")
-        selected = np.sort(observed[ranked[:254]]).astype("<u2")
-        candidates = len(selected)
-        while len(selected):
-            vocab = selected.tobytes()
-            mixed = huff0.build_mixed_codebook(huff0.count_mixed_tokens(samples, vocab), vocab,
-                                               prior_count=self.prior_count)
-            lengths = np.frombuffer(mixed.codebook[4:], dtype=np.uint8).astype(np.uint16)
-            keep = lengths[256:] <= lengths[selected & 255] + lengths[selected >> 8]
-            if keep.all():
-                scores = self._compare_codebooks(group, spec, singleton, mixed, vocab)
-                scores.update(candidate_pairs=candidates, kept_pairs=len(selected))
-                if scores["mode"] == "mixed_huffman":
-                    return mixed, vocab, scores
-                return singleton, b"", scores
-            selected = selected[keep]
-        return singleton, b"", None
-
-    def _compare_codebooks(self, group, spec, singleton, mixed, vocab):
-        """Encoded size (and time) of up to four sample chunks with each code,
-        scaled to the cluster's weight plus the codebook's metadata
-        (setup.py:207-249)."""
-        available = group["samples"]
-        picks = np.linspace(0, len(available) - 1, min(4, len(available)), dtype=int)
-        samples = [available[i] for i in picks]
-        data = []
-        for sample in samples:
-            lanes = np.zeros(len(sample) * spec.element_size, dtype=np.uint8)
-            lanes[group["stream"]::spec.element_size] = np.frombuffer(sample, dtype=np.uint8)
-            data.append(np.frombuffer(spec.reorder_bytes(lanes.tobytes(), restore=True), dtype=np.uint8))
-        options = (singleton, mixed)
-        modes = ("shared_huff0" if singleton is not None else "raw", "mixed_huffman")
-        specs = [tuple((raw, spec, group["stream"], _stream_chunk_size(self.chunk_size, spec.element_size),
-                        ({"kind": mode, "codebook": book, "codebook_id": 0} if book is not None else {"kind": "raw"},))
-                       for raw in data) for book, mode in zip(options, modes)]
-        timings, sizes, used = [[], []], [0, 0], [False, False]
-        for repeat in range(6):
-            for index in ((0, 1) if repeat % 2 == 0 else (1, 0)):
-                (output, groups), seconds = time_call(
-                    huff0.compress_direct_storage, specs[index], b"", threads=1,
-                    min_saving_bytes=self.min_saving_bytes, compression_threshold=self.compression_threshold)
-                if repeat:
-                    timings[index].append(seconds)
-                lane_chunks = [chunk for streams in groups for chunk in streams[group["stream"]]]
-                sizes[index] = sum(chunk[4] + CHUNK_METADATA_BYTES[chunk[0]] for chunk in lane_chunks)
-                used[index] = any(chunk[0] != "raw" for chunk in lane_chunks)
-                del output
-        sampled = sum(map(len, samples))
-        for index, (book, mode, vocabulary) in enumerate(zip(options, modes, (b"", vocab))):
-            overhead = 0 if book is None or not used[index] else CodebookPayload(
-                0, group["stream"], spec.name, mode, book.codebook, vocab=vocabulary).metadata_bytes
-            sizes[index] = sizes[index] * group["weight"] / sampled + overhead
-        keep = sizes[1] < sizes[0]
-        return {"mode": "mixed_huffman" if keep else modes[0],
-                "singleton_bytes_estimate": sizes[0], "mixed_bytes_estimate": sizes[1],
-                "singleton_seconds": median(timings[0]), "mixed_seconds": median(timings[1])}
+            value = _SetupUnpickler(io.BytesIO(Path(value).read_bytes())).load()
+        if isinstance(value, cls) and hasattr(value, "chunk_codebooks"):
+            return value
+        raise TypeError("Expected a current chunk-level NeuralZip setup.")

@@ -395,14 +395,15 @@ def test_grouped_products_after_the_first_step_fit_their_partials():
     import transformers
     from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
     from neuralzip_amd.setup import NeuralZipSetup
-    config = transformers.LlamaConfig(hidden_size=1024, intermediate_size=4096, num_hidden_layers=2,
-                                      num_attention_heads=8, num_key_value_heads=2, vocab_size=256,
+    config = transformers.LlamaConfig(hidden_size=2048, intermediate_size=8192, num_hidden_layers=2,
+                                      num_attention_heads=16, num_key_value_heads=4, vocab_size=256,
                                       max_position_embeddings=128, tie_word_embeddings=False)
     torch.manual_seed(3)
     model = transformers.LlamaForCausalLM(config).to(torch.bfloat16).eval()
     reference = copy.deepcopy(model).cuda()
     setup = NeuralZipSetup().build(model)
     runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", matvec_tokens=2)
+    assert {"model.layers.0", "model.layers.1", "lm_head"} <= runtime._matvec_blocks
     single = max(2 * plan.n_tiles for plan in runtime._matvec.values()) * 2
     ids = torch.randint(0, 256, (2, 16), generator=torch.Generator().manual_seed(4)).cuda()
     with torch.no_grad():

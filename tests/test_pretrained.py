@@ -16,12 +16,12 @@ from neuralzip_amd.gpu import pretrained
 def patched():
     save, load = PreTrainedModel.save_pretrained, PreTrainedModel.__dict__["from_pretrained"]
     fields = ("save", "load", "setup", "device", "matvec_tokens")
-    state = tuple(getattr(pretrained._Patch, f) for f in fields)
+    state = tuple(getattr(pretrained._STATE, f) for f in fields)
     yield
     PreTrainedModel.save_pretrained = save
     PreTrainedModel.from_pretrained = load
     for f, value in zip(fields, state):
-        setattr(pretrained._Patch, f, value)
+        setattr(pretrained._STATE, f, value)
 
 
 def tiny_llama(tie=False, seed=0):
@@ -103,7 +103,7 @@ def test_enable_is_idempotent(patched):
     first = PreTrainedModel.save_pretrained
     neuralzip(device="cuda:0")
     assert PreTrainedModel.save_pretrained is first
-    assert pretrained._Patch.device == "cuda:0"
+    assert pretrained._STATE.device == "cuda:0"
 
 
 @pytest.mark.gpu
