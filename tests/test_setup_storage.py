@@ -104,3 +104,106 @@ def test_selected_lane_is_the_reordered_lane(dtype):
     reordered = np.frombuffer(spec.reorder_bytes(raw), dtype=np.uint8)
     expected = reordered[spec.selected_stream::spec.element_size]
     assert np.array_equal(spec.selected_lane(raw), expected)
+
+
+def _exponent_counts(rng, centre, spread, n=4096):
+    """A chunk's exponent-field histogram: values around `centre`."""
+    values = np.clip(np.round(rng.normal(centre, spread, n)), 0, 255).astype(np.int64)
+    return np.bincount(values, minlength=256)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_native_clustering_matches_the_oracle(shared):
+    """nz_clusterer against oracle/setup_ref.py (a restatement of
+    setup.py:91-141) on chunks of two dtypes, scattered scales and forced
+    labels: the same cluster for every chunk, in the same numbering."""
+    from oracle import setup_ref
+    from neuralzip_amd import _native
+    rng = np.random.default_rng(11)
+    chunks = []
+    for i in range(300):
+        dtype = ("bfloat16", "float32")[i % 7 == 3]
+        label = (None, None, None, "a", 2)[int(rng.integers(0, 5))] if i % 5 == 0 else None
+        counts = _exponent_counts(rng, 120 + 4 * rng.integers(-3, 4), 1.0 + rng.random() * 3)
+        chunks.append((dtype, label, counts, int(rng.integers(1000, 70000))))
+    want, _ = setup_ref.cluster(chunks, 0.05, shared)
+    engine = _native.Clusterer(0.05, shared)
+    labels = {None: -1, "a": 0, 2: 1}
+    got = []
+    # fed as the setup feeds it: runs of chunks of one dtype
+    start = 0
+    while start < len(chunks):
+        end = start
+        while end < len(chunks) and chunks[end][0] == chunks[start][0]:
+            end += 1
+        part = chunks[start:end]
+        got += engine.assign(np.stack([c[2] for c in part]).astype(np.uint32),
+                             ("bfloat16", "float32").index(part[0][0]),
+                             [labels[c[1]] for c in part], [c[3] for c in part]).tolist()
+        start = end
+    assert got == want
+    assert len(engine) == max(want) + 1
+
+
+def test_native_clustering_threshold_decides_like_the_oracle_at_the_edge():
+    """Two chunks whose distance the oracle computes as d: with the
+    threshold just above d they share a cluster, just below they do not (a
+    wrong distance formula or summation flips one of them)."""
+    from oracle import setup_ref
+    from neuralzip_amd import _native
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        a, b = _exponent_counts(rng, 120, 2.0), _exponent_counts(rng, 121, 2.5)
+        d = setup_ref.js_distance(a / a.sum(), b / b.sum())
+        for threshold, joined in ((d * (1 + 1e-12), True), (d * (1 - 1e-12), False)):
+            engine = _native.Clusterer(threshold)
+            got = engine.assign(np.stack([a, b]).astype(np.uint32), 0, [-1, -1], [4096, 4096]).tolist()
+            assert got == ([0, 0] if joined else [0, 1]), (d, threshold)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_chunk_histograms_match_numpy(dtype):
+    """Per-chunk exponent-field counts and pooled selected-lane counts of
+    the native survey against numpy over the reordered words (dtypes.py)."""
+    from neuralzip_amd import _native
+    from neuralzip_amd.dtypes import DTYPES
+    spec = DTYPES[dtype]
+    g = torch.Generator().manual_seed(2)
+    t = (torch.randn(1000, 37, generator=g) * 0.03).to(dtype)
+    t.view(-1)[::97] = float("inf")
+    words = t.view(torch.uint8).numpy().reshape(-1)
+    step = 4099
+    fields, lanes = _native.chunk_histograms(words, spec, step)
+    exps = spec.extract_exponents(words.tobytes())
+    for c in range(len(fields)):
+        assert np.array_equal(fields[c], np.bincount(exps[c * step:(c + 1) * step], minlength=256))
+    reordered = np.frombuffer(spec.reorder_bytes(words.tobytes()), dtype=np.uint8)
+    assert np.array_equal(lanes, np.bincount(reordered[spec.selected_stream::spec.element_size], minlength=256))
+
+
+def test_setup_survey_clusters_like_the_oracle():
+    """NeuralZipSetup's survey over a model (tensors by name, chunks in
+    order, cluster_map labels) gives the oracle's clustering."""
+    from oracle import setup_ref
+    from neuralzip_amd.dtypes import DTYPES
+    from neuralzip_amd.setup import _Survey
+    g = torch.Generator().manual_seed(9)
+    named = {f"t{i}": (torch.randn(300, 400 + 10 * i, generator=g) * s).to(dt)
+             for i, (s, dt) in enumerate([(0.005, torch.bfloat16), (0.02, torch.bfloat16), (0.1, torch.float32),
+                                          (0.02, torch.float16), (0.005, torch.bfloat16)])}
+    setup = NeuralZipSetup(chunk_size=32768, cluster_map={"t1": "x", ("t4", 1): "x"})
+    survey = _Survey(setup)
+    chunks = []
+    for name in sorted(named):
+        t = named[name]
+        survey.add(name, t)
+        spec = DTYPES[t.dtype]
+        exps = spec.extract_exponents(t.view(torch.uint8).numpy().tobytes())
+        step = 32768 // spec.element_size
+        for c, lo in enumerate(range(0, t.numel(), step)):
+            label = setup.cluster_map.get((name, c), setup.cluster_map.get(name))
+            chunks.append((spec.name, label, np.bincount(exps[lo:lo + step], minlength=256), len(exps[lo:lo + step])))
+    want, clusters = setup_ref.cluster(chunks, setup.cluster_js_threshold)
+    got = [c for name in sorted(named) for key, ids in survey.chunk_clusters.items() if key[0] == name for c in ids]
+    assert got == want
+    assert [(c.dtype, c.label, c.weight) for c in survey.clusters] == [(d, l, w) for d, l, _, w in clusters]
