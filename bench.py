@@ -15,6 +15,7 @@ way) and a CPU baseline (the oracle's threaded storage decode of the same
 tensors on this host).
 """
 import argparse
+import contextlib
 import json
 import os
 import statistics
@@ -76,10 +77,12 @@ def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
     for (name, t), data in zip(tensors.items(), out):
         if bytes(data) != t.view(torch.uint8).numpy().tobytes():
             raise RuntimeError(f"oracle decode of {name} is not bit-exact")
-    med = statistics.median(times)
-    return {"value": round(decoded / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"full workload, {len(times)} timed decodes (median) after {warmups} warmups, "
-                      f"{decoded} bytes decoded each"}
+    rates = sorted(decoded / t / 1e9 for t in times)
+    q1, _, q3 = statistics.quantiles(rates, n=4) if len(rates) > 1 else (rates[0],) * 3
+    return {"value": round(statistics.median(rates), 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "iqr": [round(q1, 3), round(q3, 3)],
+            "sample": f"full workload, {len(times)} timed decodes (median, interquartile range) after {warmups} "
+                      f"warmups, {decoded} bytes decoded each"}
 
 
 def host_description():
@@ -206,50 +209,105 @@ def time_generate(model, ids, new_tokens):
     return full - first, out
 
 
-def model_benchmark(args):
-    """tok/s of greedy generation on a model shape of MODELS, NeuralZip
-    runtime against the same model uncompressed (bf16 or fp16), with the prompt's
-    logits and every generated token compared bit for bit."""
+def graph_generate(model, ids, new_tokens, runtime=None):
+    """Greedy decoding with a static KV cache whose steps are replayed from
+    one HIP graph: the prompt and the first two steps run eagerly, the graph
+    captures one step (with the runtime attached, its decode launches and
+    side-stream prefetches included) and the remaining new_tokens - 3 steps
+    are replays. Returns (seconds of the replayed steps, their count, the
+    generated ids (batch, new_tokens))."""
+    from transformers import StaticCache
+    device = ids.device
+    batch, prompt = ids.shape
+    cache = StaticCache(config=model.config, max_cache_len=prompt + new_tokens + 2)
+    generated = []
+    with torch.no_grad():
+        logits = model(input_ids=ids, past_key_values=cache, cache_position=torch.arange(prompt, device=device),
+                       use_cache=True).logits
+        token = logits[:, -1:].argmax(-1)
+        generated.append(token.clone())
+        position = torch.tensor([prompt], device=device)
+
+        def step():
+            return model(input_ids=token, past_key_values=cache, cache_position=position,
+                         use_cache=True).logits[:, -1:].argmax(-1)
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                nxt = step()
+                generated.append(nxt.clone())
+                token.copy_(nxt)
+                position += 1
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize(device)
+        graph = torch.cuda.CUDAGraph()
+        capture = runtime.graph_capture() if runtime is not None else contextlib.nullcontext()
+        with capture, torch.cuda.graph(graph):
+            out = step()
+        torch.cuda.synchronize(device)
+        replays = new_tokens - 3
+        t0 = time.perf_counter()
+        for _ in range(replays):
+            graph.replay()
+            generated.append(out.clone())
+            token.copy_(out)
+            position += 1
+        torch.cuda.synchronize(device)
+        seconds = time.perf_counter() - t0
+    del graph
+    return seconds, replays, torch.cat(generated, dim=1)
+
+
+def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=None, new_tokens=None, graph=True):
+    """Greedy generation on a model shape of MODELS, uncompressed and with the
+    NeuralZip runtime attached, on one GPU: eager Transformers generation
+    (the reference's protocol: host-bound at small batches) and, with
+    `graph`, decode steps replayed from a HIP graph (device-bound). The
+    prompt's logits and all generated tokens are compared bit for bit.
+    Returns the JSON line of the model benchmark."""
     from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu
     from neuralzip_amd.setup import NeuralZipSetup
     device = torch.device("cuda:0")
-    _, shape, _, default_prompt, default_new, description = MODELS[args.model]
-    prompt = args.prompt or default_prompt
-    new_tokens = args.new_tokens or default_new
+    _, shape, _, default_prompt, default_new, description = MODELS[kind]
+    prompt = prompt or default_prompt
+    new_tokens = new_tokens or default_new
     t0 = time.perf_counter()
-    dtype = WEIGHT_DTYPES[args.dtype]
-    description = description.format(dtype=args.dtype)
-    model = random_model(args.model, device, dtype)
-    log(f"model built in {time.perf_counter() - t0:.1f}s")
-    ids = torch.randint(0, shape["vocab_size"], (args.batch, prompt),
-                        generator=torch.Generator().manual_seed(3)).to(device)
+    dtype = WEIGHT_DTYPES[dtype_name]
+    description = description.format(dtype=dtype_name)
+    model = random_model(kind, device, dtype)
+    log(f"{kind}: model built in {time.perf_counter() - t0:.1f}s")
+    ids = torch.randint(0, shape["vocab_size"], (batch, prompt), generator=torch.Generator().manual_seed(3)).to(device)
     with torch.no_grad():
         ref_logits = model(ids[:, :64]).logits.float().cpu()
     torch.cuda.reset_peak_memory_stats(device)
     base_s, base_out = time_generate(model, ids, new_tokens)
     base_peak = torch.cuda.max_memory_allocated(device)
-    log(f"{args.dtype}: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {base_peak / 2**30:.1f} GiB")
+    log(f"{dtype_name}: {base_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {base_peak / 2**30:.1f} GiB")
+    base_graph = graph_generate(model, ids, new_tokens) if graph else None
+    if base_graph:
+        log(f"{dtype_name} graph: {base_graph[0] / base_graph[1] * 1e3:.3f} ms per replayed step")
     t0 = time.perf_counter()
-    # setup and export read each weight back from the device one at a time
     marks = {}
 
     def progress(done, total, name):
         decile = 10 * done // total
         if decile not in marks:
             marks[decile] = True
-            log(f"setup: {done}/{total} tensors clustered ({time.perf_counter() - t0:.0f}s)")
+            log(f"setup: {done}/{total} tensors surveyed ({time.perf_counter() - t0:.0f}s)")
     setup = NeuralZipSetup(cluster_js_threshold=0.05).build(model, progress=progress)
-    log(f"setup: {len(setup.codebooks)} codebooks in {time.perf_counter() - t0:.1f}s")
+    setup_s = time.perf_counter() - t0
+    log(f"setup: {len(setup.codebooks)} codebooks in {setup_s:.1f}s")
     t0 = time.perf_counter()
     exported = export_model_for_gpu(model, setup)
-    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=args.matvec,
-                                      decode_slots=args.slots)
-    log(f"export + attach: {len(exported.groups)} fragments, {len(exported.block_order)} blocks "
-        f"in {time.perf_counter() - t0:.1f}s")
+    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=matvec, decode_slots=slots)
+    attach_s = time.perf_counter() - t0
+    log(f"export + attach: {len(exported.groups)} fragments, {len(exported.block_order)} blocks in {attach_s:.1f}s")
     with torch.no_grad():
         logits = model(ids[:, :64]).logits.float().cpu()
     # one decode of every compressed block, back to back on one stream
     stream = torch.cuda.current_stream(device)
+    runtime.drain()
     for name in exported.block_order:
         runtime._launch(name, stream)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -268,7 +326,10 @@ def model_benchmark(args):
     nz_s, nz_out = time_generate(model, ids, new_tokens)
     nz_peak = torch.cuda.max_memory_allocated(device)
     log(f"neuralzip: {nz_s * 1e3:.1f} ms for {new_tokens - 1} decode steps, peak {nz_peak / 2**30:.1f} GiB")
-    matvec = {}
+    nz_graph = graph_generate(model, ids, new_tokens, runtime) if graph else None
+    if nz_graph:
+        log(f"neuralzip graph: {nz_graph[0] / nz_graph[1] * 1e3:.3f} ms per replayed step")
+    matvec_info = {}
     if runtime._matvec:
         # one pass of fused products over every compressed Linear (one
         # activation row), using the groups generation learned
@@ -290,17 +351,29 @@ def model_benchmark(args):
         weights = sum(p.rows * p.cols * torch.empty((), dtype=p.dtype).element_size() for p in plans)
         reads = sum(p.algorithmic_bytes for p in plans)
         log(f"full fused matvec pass: {mv_ms:.3f} ms in {len(plans)} products ({len(runtime._group_plans)} groups), "
-            f"{reads / mv_ms / 1e6:.0f} GB/s read, {weights / mv_ms / 1e6:.0f} GB/s of {args.dtype} weights")
-        matvec = {"fused_matvec_tokens": args.matvec, "full_matvec_pass_ms": round(mv_ms, 3),
-                  "full_matvec_pass_read_gbps": round(reads / mv_ms / 1e6, 1),
-                  "full_matvec_pass_weight_gbps": round(weights / mv_ms / 1e6, 1),
-                  "fused_products_per_pass": len(plans), "fused_groups": len(runtime._group_plans),
-                  "fused_blocks": len(runtime._matvec_blocks)}
+            f"{reads / mv_ms / 1e6:.0f} GB/s read, {weights / mv_ms / 1e6:.0f} GB/s of {dtype_name} weights")
+        matvec_info = {"fused_matvec_tokens": matvec, "full_matvec_pass_ms": round(mv_ms, 3),
+                       "full_matvec_pass_read_gbps": round(reads / mv_ms / 1e6, 1),
+                       "full_matvec_pass_weight_gbps": round(weights / mv_ms / 1e6, 1),
+                       "fused_products_per_pass": len(plans), "fused_groups": len(runtime._group_plans),
+                       "fused_blocks": len(runtime._matvec_blocks)}
     steps = new_tokens - 1
-    tok_s = args.batch * steps / nz_s
-    base_tok_s = args.batch * steps / base_s
+    tok_s = batch * steps / nz_s
+    base_tok_s = batch * steps / base_s
+    graph_info = None
+    if graph:
+        g_nz = batch * nz_graph[1] / nz_graph[0]
+        g_base = batch * base_graph[1] / base_graph[0]
+        graph_info = {"neuralzip_tok_s": round(g_nz, 2), "uncompressed_tok_s": round(g_base, 2),
+                      "ratio_vs_uncompressed": round(g_base / g_nz, 3),
+                      "neuralzip_ms_per_step": round(nz_graph[0] / nz_graph[1] * 1e3, 3),
+                      "uncompressed_ms_per_step": round(base_graph[0] / base_graph[1] * 1e3, 3),
+                      "replayed_steps": nz_graph[1],
+                      "tokens_identical_to_uncompressed": bool(torch.equal(nz_graph[2].cpu(), base_graph[2].cpu())),
+                      "tokens_identical_to_eager": bool(torch.equal(base_graph[2].cpu(),
+                                                                    base_out[:, prompt:].cpu()))}
     line = {
-        "metric": f"tok/s {args.model} shape bs={args.batch} vs uncompressed {args.dtype}",
+        "metric": f"tok/s {kind} shape bs={batch} vs uncompressed {dtype_name}",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -310,30 +383,58 @@ def model_benchmark(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": args.dtype,
+        "dtype": dtype_name,
         "data": "synthetic",
-        "config": {"workload": f"{description}, greedy generation, batch {args.batch}, {prompt} prompt + "
+        "config": {"workload": f"{description}, greedy generation, batch {batch}, {prompt} prompt + "
                                f"{new_tokens} new tokens, decode phase timed",
                    "compressed_blocks": len(exported.block_order),
                    "full_decode_pass_ms": round(pass_ms, 3),
                    "full_decode_pass_gbps": round(decoded_bytes / pass_ms / 1e6, 1),
                    "decoded_bytes_per_pass": int(decoded_bytes),
                    "compressed_store_bytes": int(runtime.store.nbytes),
+                   "setup_seconds": round(setup_s, 1), "export_attach_seconds": round(attach_s, 1),
                    "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
-                   "prefetch": runtime.prefetch, "decode_slots": args.slots or "one per CU", **matvec},
+                   "prefetch": runtime.prefetch, "decode_slots": slots or "one per CU", **matvec_info},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
+        "graph": graph_info,
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
         "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
         # generated tokens before the first position where any sequence differs
         "matching_token_prefix": int((nz_out[:, prompt:].cpu() == base_out[:, prompt:].cpu()).all(0).int()
                                      .cumprod(0).sum()),
     }
+    del runtime, model, exported
+    torch.cuda.empty_cache()
+    return line
+
+
+def model_benchmark(args):
+    line = run_model(args.model, args.batch, args.dtype, args.matvec, args.slots, args.prompt, args.new_tokens,
+                     graph=not args.no_graph)
     print(json.dumps(line), flush=True)
+    exact = line["logits_bitwise_equal"] and (line["tokens_identical"] or args.matvec)
+    if line["graph"] and not args.matvec:
+        exact = exact and line["graph"]["tokens_identical_to_uncompressed"]
     # fused products are not bit-identical to the GEMM, so generated tokens may differ there
-    return 0 if line["logits_bitwise_equal"] and (line["tokens_identical"] or args.matvec) else 1
+    return 0 if exact else 1
+
+
+def model_summary(line):
+    """The model benchmark's figures carried in the default bench line."""
+    return {"workload": line["config"]["workload"],
+            "eager": {"neuralzip_tok_s": line["value"], "uncompressed_tok_s": line["uncompressed_tok_s"],
+                      "ratio_vs_uncompressed": line["ratio_vs_uncompressed"],
+                      "ms_per_step": line["ms_per_step"]},
+            "graph": line["graph"],
+            "full_decode_pass_ms": line["config"]["full_decode_pass_ms"],
+            "full_decode_pass_gbps": line["config"]["full_decode_pass_gbps"],
+            "logits_bitwise_equal": line["logits_bitwise_equal"],
+            "tokens_identical": line["tokens_identical"],
+            "peak_allocated_uncompressed_gib": line["config"]["peak_allocated_uncompressed_gib"],
+            "peak_allocated_neuralzip_gib": line["config"]["peak_allocated_neuralzip_gib"]}
 
 
 def main():
@@ -357,6 +458,9 @@ def main():
                              "(0: always decode)")
     parser.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the model's)")
     parser.add_argument("--new-tokens", type=int, default=None, help="generated tokens (default: the model's)")
+    parser.add_argument("--no-graph", action="store_true", help="model benchmark: eager generation only")
+    parser.add_argument("--no-model", action="store_true",
+                        help="default run: leave out the Llama-3-8B-shape bs=1 tok/s part of the line")
     args = parser.parse_args()
     if args.copy_calibration:
         return copy_calibration()
@@ -369,6 +473,13 @@ def main():
         print("bench.py measures one GPU: decode needs no collective and this build runs on one device; "
               "run with --gpus 1.", file=sys.stderr)
         return 2
+
+    model = None
+    if not args.no_model:
+        # the tok/s half of the metric: Llama-3-8B shape, batch 1, bit-exact decode path
+        model = model_summary(run_model("llama3-8b", graph=not args.no_graph))
+        log(f"model: eager ratio {model['eager']['ratio_vs_uncompressed']}, graph ratio "
+            f"{model['graph']['ratio_vs_uncompressed'] if model['graph'] else None}")
 
     from neuralzip_amd.dtypes import DTYPES
     from neuralzip_amd.gpu import decoder as gpu_decoder
@@ -406,6 +517,20 @@ def main():
     decoded_bytes = sum(int(d["numel"]) for d in store.descs) * spec.element_size
     stream = torch.cuda.current_stream(device)
 
+    # bit-exactness of one step, checked before the timed steps
+    if set(offsets) != set(tensors):
+        raise RuntimeError("every tensor of the workload must be GPU-compressed")
+    workspace.view(torch.uint8).fill_(0xA5)
+    for batch in batches:
+        decoder.decode_batch(batch, stream)
+    for name, t in tensors.items():
+        off = offsets[name]
+        got = workspace[off:off + t.numel()].view(torch.uint8).cpu()
+        if not torch.equal(got, t.reshape(-1).view(torch.uint8)):
+            raise RuntimeError(f"GPU decode of {name} is not bit-exact")
+    achievable = copy_bandwidth(device)
+    log(f"bit-exact; device copy {achievable:.0f} GB/s")
+
     for _ in range(args.warmup):
         for batch in batches:
             decoder.decode_batch(batch, stream)
@@ -432,20 +557,11 @@ def main():
         launch_ms.append(a.elapsed_time(b) / args.steps)
     dominant = max(range(len(batches)), key=lambda k: launch_ms[k])
     achieved = batches[dominant].algorithmic_bytes / (launch_ms[dominant] * 1e-3) / 1e9
+    log(f"{ms_per_step:.4f} ms/step, launches {[round(m, 4) for m in launch_ms]} ms")
 
-    # bit-exactness of the final step
-    if set(offsets) != set(tensors):
-        raise RuntimeError("every tensor of the workload must be GPU-compressed")
-    for name, t in tensors.items():
-        off = offsets[name]
-        got = workspace[off:off + t.numel()].view(torch.uint8).cpu()
-        if not torch.equal(got, t.reshape(-1).view(torch.uint8)):
-            raise RuntimeError(f"GPU decode of {name} is not bit-exact")
-    log(f"bit-exact; {ms_per_step:.4f} ms/step, launches {[round(m, 4) for m in launch_ms]} ms")
-
-    achievable = copy_bandwidth(device)
-    log(f"device copy {achievable:.0f} GB/s")
-
+    # HBM bytes per launch come from rocprofv3 counter runs of this workload
+    # (FETCH_SIZE and WRITE_SIZE, calibrated by a plain copy), committed under
+    # profiles/; they cannot be read from inside this process
     traffic = None
     traffic_file = ROOT / "profiles" / "decode_traffic.json"
     if traffic_file.exists():
@@ -456,9 +572,9 @@ def main():
         threads = min(os.cpu_count() or 1, 16)
         baseline = cpu_baseline(tensors, setup, threads)
         log(f"cpu baseline {baseline['value']} GB/s on {threads} threads")
-        single = cpu_baseline(tensors, setup, 1, reps=3, warmups=1, budget_s=10.0)
+        single = cpu_baseline(tensors, setup, 1, budget_s=20.0)
         log(f"cpu baseline {single['value']} GB/s on 1 thread")
-        baseline["single_thread"] = {"value": single["value"], "unit": single["unit"], "sample": single["sample"]}
+        baseline["single_thread"] = {k: single[k] for k in ("value", "unit", "iqr", "sample")}
         baseline["host"] = host_description()
 
     line = {
@@ -472,7 +588,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
             "workload": WORKLOAD,
@@ -491,12 +607,16 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": "profiles/decode_traffic.json: rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this launch",
             "copy_achievable": round(achievable, 1),
             "frac_of_copy": round(achieved / achievable, 4),
         },
         "cpu_baseline": baseline,
+        "model": model,
     }
     print(json.dumps(line), flush=True)
+    if model is not None and not (model["logits_bitwise_equal"] and model["tokens_identical"]):
+        return 1
     return 0
 
 

@@ -166,6 +166,20 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
                      uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
                      void* stream);
 
+/* Flags of nz_decode_launch_ex. */
+#define NZ_DECODE_CACHED_STORES 1u   /* ordinary output stores (default: streaming) */
+
+/* nz_decode_launch with flags. NZ_DECODE_CACHED_STORES writes the decoded
+ * words with ordinary stores, which leave them in the L2 and the Infinity
+ * Cache for a consumer that runs right after the decode (a weight decoded
+ * just before its own GEMM); the default streaming stores suit decodes
+ * whose output is read later. Same reference counterpart as
+ * nz_decode_launch (decoder.py:193-208), whose kernel always stores through
+ * the caches. */
+int nz_decode_launch_ex(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
+                        uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
+                        uint32_t flags, void* stream);
+
 /* CPU emulation of nz_decode_launch on host copies of the same arrays; a
  * test hook for GPU-less hosts, never used by the runtime. */
 int nz_emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,

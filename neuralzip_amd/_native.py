@@ -98,6 +98,7 @@ def lib():
         L.nz_plan_work_interleaved.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32), vp]
         L.nz_decode_slots.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.nz_decode_launch_ex.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         L.nz_matvec_plan.argtypes = [vp, vp, u32, vp, u32, u32, ctypes.c_int, vp, vp, u32, ctypes.POINTER(u32)]
         L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, u32,
@@ -243,10 +244,15 @@ def decode_slots(element_size, bit_reorder, long_codes):
     return n.value
 
 
+# nz_decode_launch_ex flag: ordinary output stores (the words stay in the caches)
+DECODE_CACHED_STORES = 1
+
+
 def decode_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, element_size, bit_reorder, long_codes,
-                  out_ptr, stream_ptr):
-    check(lib().nz_decode_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, int(n_segments), int(element_size),
-                                 int(bit_reorder), int(long_codes), out_ptr, stream_ptr))
+                  out_ptr, stream_ptr, flags=0):
+    check(lib().nz_decode_launch_ex(base_ptr, frags_ptr, tiles_ptr, segments_ptr, int(n_segments),
+                                    int(element_size), int(bit_reorder), int(long_codes), out_ptr, int(flags),
+                                    stream_ptr))
 
 
 def emulate_decode(base, descs, tiles, segments, element_size, bit_reorder, out):

@@ -37,7 +37,7 @@ using nz_capi::set_error;
 
 extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes, void* out,
-                                    void* stream, char* message, size_t message_size);
+                                    int cached, void* stream, char* message, size_t message_size);
 extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_codes, int* out, char* message,
                                    size_t message_size);
 extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
@@ -217,16 +217,25 @@ int nz_decode_slots(int element_size, int bit_reorder, int long_codes, int* slot
     return 0;
 }
 
+int nz_decode_launch_ex(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
+                        uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
+                        uint32_t flags, void* stream) {
+    if (n_segments && (!base || !frags || !tiles || !segments || !out))
+        return set_error(nz::kInvalidArgument, "Null decode argument.");
+    if (flags & ~uint32_t(NZ_DECODE_CACHED_STORES)) return set_error(nz::kInvalidArgument, "Unknown decode flags.");
+    char message[256] = {0};
+    const int rc = nz_hip_decode_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
+                                        long_codes, out, (flags & NZ_DECODE_CACHED_STORES) != 0, stream, message,
+                                        sizeof message);
+    if (rc) return set_error(rc, message);
+    return 0;
+}
+
 int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
                      uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
                      void* stream) {
-    if (n_segments && (!base || !frags || !tiles || !segments || !out))
-        return set_error(nz::kInvalidArgument, "Null decode argument.");
-    char message[256] = {0};
-    const int rc = nz_hip_decode_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
-                                        long_codes, out, stream, message, sizeof message);
-    if (rc) return set_error(rc, message);
-    return 0;
+    return nz_decode_launch_ex(base, frags, tiles, segments, n_segments, element_size, bit_reorder, long_codes, out,
+                               0, stream);
 }
 
 int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,

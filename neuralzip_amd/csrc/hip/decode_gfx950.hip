@@ -67,8 +67,10 @@ __device__ __forceinline__ void store_element(rsrc_t out, uint32_t offset, uint3
 }
 
 
-// Decodes a tile and stores its words into the workspace `out`.
-template <int ES, bool REORDER, bool LONG, bool ESC>
+// Decodes a tile and stores its words into the workspace `out`: streaming
+// (nontemporal) stores, or, with CACHED, ordinary stores that leave the words
+// in the caches for a consumer that runs right after the decode.
+template <int ES, bool REORDER, bool LONG, bool ESC, bool CACHED>
 __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES, LONG>& d, const uint32_t* lut,
                                              uint8_t* stage, uint32_t lane, uint8_t* out_base) {
     using G = Geometry<ES>;
@@ -94,7 +96,7 @@ __device__ __forceinline__ void huffman_tile(const TileInfo& ti, const Fetch<ES,
         }
         const uint4 v = merge_vector<ES, REORDER>(e0, e1, d.raw[r]);
         const v4u vv = {v.x, v.y, v.z, v.w};
-        __builtin_amdgcn_raw_buffer_store_b128(vv, out, whole ? g * ES : kOutOfRange, 0, kNonTemporal);
+        __builtin_amdgcn_raw_buffer_store_b128(vv, out, whole ? g * ES : kOutOfRange, 0, CACHED ? 0 : kNonTemporal);
     }
     if (ti.s0 != 0 || ti.s1 % V != 0) {   // elements of the partial first and last vectors (fragment ends)
         const uint32_t g = edge_index<ES>(ti, lane);
@@ -150,7 +152,7 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
 
 // One wavefront's share of a Huffman segment: claim tiles until the segment
 // is used up, fetching (and claiming) one tile ahead of the one it decodes.
-template <int ES, bool REORDER, bool LONG, bool ESC>
+template <int ES, bool REORDER, bool LONG, bool ESC, bool CACHED>
 __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
                                                 const nz_work& seg, uint32_t* counter, uint32_t lane,
                                                 const uint32_t* lut, uint8_t* stage, uint8_t* out) {
@@ -167,7 +169,7 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_fr
         Fetch<ES, LONG> fn;
         fetch<ES, LONG>(nxt, lane, fn);
         const uint32_t after = more ? claim(counter, lane) : n;
-        huffman_tile<ES, REORDER, LONG, ESC>(cur, fc, lut, stage, lane, out);
+        huffman_tile<ES, REORDER, LONG, ESC, CACHED>(cur, fc, lut, stage, lane, out);
         if (!more) break;
         t = tn;
         tn = after;
@@ -190,7 +192,7 @@ __device__ __forceinline__ void raw_segment(const uint8_t* base, const nz_frag_d
 // Launch: one workgroup per segment (segments are cut to equal work, about
 // as many as the device runs at once); its wavefronts claim the segment's
 // tiles one at a time, so a wavefront with cheap tiles takes more of them.
-template <int ES, bool REORDER, bool LONG>
+template <int ES, bool REORDER, bool LONG, bool CACHED>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NZ_WAVES_PER_EU)))
 void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
                       const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs,
@@ -218,24 +220,30 @@ void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
     // Codebooks whose codes all fit the primary table run the loop without
     // the escape check (long-code codebooks always have escapes).
     if constexpr (LONG) {
-        huffman_segment<ES, REORDER, true, true>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave], out);
+        huffman_segment<ES, REORDER, true, true, CACHED>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave],
+                                                         out);
     } else {
         if (s_lut[0])
-            huffman_segment<ES, REORDER, false, true>(base, frags, tiles, seg, &s_claim, lane, s_lut,
-                                                      s_stage[wave], out);
+            huffman_segment<ES, REORDER, false, true, CACHED>(base, frags, tiles, seg, &s_claim, lane, s_lut,
+                                                              s_stage[wave], out);
         else
-            huffman_segment<ES, REORDER, false, false>(base, frags, tiles, seg, &s_claim, lane, s_lut,
-                                                       s_stage[wave], out);
+            huffman_segment<ES, REORDER, false, false, CACHED>(base, frags, tiles, seg, &s_claim, lane, s_lut,
+                                                               s_stage[wave], out);
     }
 }
 
 template <int ES, bool REORDER, bool LONG>
 hipError_t launch(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
-                  void* out, hipStream_t stream) {
-    hipLaunchKernelGGL((nz_decode_kernel<ES, REORDER, LONG>), dim3(n_segs), dim3(kThreads), 0, stream,
-                       static_cast<const uint8_t*>(base), static_cast<const nz_frag_desc*>(frags),
-                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs),
-                       static_cast<uint8_t*>(out));
+                  void* out, bool cached, hipStream_t stream) {
+    auto args = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(n_segs), dim3(kThreads), 0, stream, static_cast<const uint8_t*>(base),
+                           static_cast<const nz_frag_desc*>(frags), static_cast<const nz_tile*>(tiles),
+                           static_cast<const nz_work*>(segs), static_cast<uint8_t*>(out));
+    };
+    if (cached)
+        args(nz_decode_kernel<ES, REORDER, LONG, true>);
+    else
+        args(nz_decode_kernel<ES, REORDER, LONG, false>);
     return hipGetLastError();
 }
 
@@ -245,7 +253,8 @@ hipError_t slots(int* out) {
     hipError_t rc = hipGetDevice(&device);
     if (rc == hipSuccess) rc = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
     if (rc == hipSuccess)
-        rc = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nz_decode_kernel<ES, REORDER, LONG>, kThreads, 0);
+        rc = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nz_decode_kernel<ES, REORDER, LONG, false>, kThreads,
+                                                          0);
     *out = cus * per_cu;
     return rc;
 }
@@ -256,11 +265,11 @@ hipError_t slots(int* out) {
 // (stream-ordered, asynchronous). Returns 0 or a negative error code.
 extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes, void* out,
-                                    void* stream, char* message, size_t message_size) {
+                                    int cached, void* stream, char* message, size_t message_size) {
     if (n_segs == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t rc;
-#define NZ_LAUNCH(E, R, L) launch<E, R, L>(base, frags, tiles, segs, n_segs, out, st)
+#define NZ_LAUNCH(E, R, L) launch<E, R, L>(base, frags, tiles, segs, n_segs, out, cached != 0, st)
     if (element_size == 2 && bit_reorder)
         rc = long_codes ? NZ_LAUNCH(2, true, true) : NZ_LAUNCH(2, true, false);
     else if (element_size == 2)

@@ -33,8 +33,9 @@ uint32_t reorder_restore(uint32_t v, unsigned m, unsigned e) {
 // enough zero padding after the last window).
 uint64_t peek64(const uint8_t* bits, uint64_t pos) {
     const uint8_t* p = bits + (pos >> 3);
-    uint64_t v = 0;
-    for (int i = 0; i < 8; ++i) v = (v << 8) | p[i];
+    uint64_t v;
+    std::memcpy(&v, p, 8);
+    v = __builtin_bswap64(v);
     const unsigned r = pos & 7;
     return r ? (v << r) | (p[8] >> (8 - r)) : v;
 }
@@ -45,6 +46,72 @@ uint32_t alignbit(uint32_t a, uint32_t b, uint32_t s) {
 
 uint32_t load_be32(const uint8_t* p) {
     return (uint32_t(p[0]) << 24) | (uint32_t(p[1]) << 16) | (uint32_t(p[2]) << 8) | p[3];
+}
+
+// The selected lane (the top byte after the reorder) into sym and the lanes
+// below it into lanes[k * stride + i] (dtypes.py:23-45 forward).
+void split_lanes(const uint8_t* src, uint32_t numel, const LaneSpec& spec, uint8_t* sym, uint8_t* lanes,
+                 uint32_t stride) {
+    const unsigned es = spec.element_size;
+    if (es == 2 && spec.bit_reorder) {   // bfloat16: exponent byte, sign | 7 mantissa bits
+        for (uint32_t i = 0; i < numel; ++i) {
+            const uint32_t v = src[2 * i] | (uint32_t(src[2 * i + 1]) << 8);
+            sym[i] = static_cast<uint8_t>(v >> 7);
+            lanes[i] = static_cast<uint8_t>((v & 0x7Fu) | ((v >> 8) & 0x80u));
+        }
+    } else if (es == 2) {                // float16: high byte, low byte
+        for (uint32_t i = 0; i < numel; ++i) {
+            sym[i] = src[2 * i + 1];
+            lanes[i] = src[2 * i];
+        }
+    } else {
+        for (uint32_t i = 0; i < numel; ++i) {
+            uint32_t v;
+            std::memcpy(&v, src + 4 * static_cast<size_t>(i), 4);
+            if (spec.bit_reorder) v = reorder_forward(v, spec.mantissa_bits, spec.exponent_bits);
+            sym[i] = static_cast<uint8_t>(v >> 24);
+            lanes[i] = static_cast<uint8_t>(v);
+            lanes[stride + i] = static_cast<uint8_t>(v >> 8);
+            lanes[2 * static_cast<size_t>(stride) + i] = static_cast<uint8_t>(v >> 16);
+        }
+    }
+}
+
+// MSB-first concatenation of the tokens' codes into `out` (zeroed, with room
+// for the whole stream plus 8 bytes): a 64-bit accumulator flushed 32 bits
+// at a time.
+void pack_codes(const uint16_t* tokens, size_t n, const uint8_t* lengths, const uint64_t* codes, uint8_t* out) {
+    uint64_t acc = 0;   // the low `held` bits are pending, oldest highest
+    unsigned held = 0;
+    auto flush32 = [&] {
+        held -= 32;
+        const uint32_t word = static_cast<uint32_t>(acc >> held);
+        out[0] = static_cast<uint8_t>(word >> 24);
+        out[1] = static_cast<uint8_t>(word >> 16);
+        out[2] = static_cast<uint8_t>(word >> 8);
+        out[3] = static_cast<uint8_t>(word);
+        out += 4;
+    };
+    for (size_t k = 0; k < n; ++k) {
+        const unsigned len = lengths[tokens[k]];
+        const uint64_t code = codes[tokens[k]];
+        if (len > 32) {   // long codes go in two parts so the accumulator never overflows
+            acc = (acc << (len - 32)) | (code >> 32);
+            held += len - 32;
+            if (held >= 32) flush32();
+            acc = (acc << 32) | (code & 0xFFFFFFFFu);
+            held += 32;
+        } else {
+            acc = (acc << len) | code;
+            held += len;
+        }
+        if (held >= 32) flush32();
+    }
+    while (held >= 8) {
+        held -= 8;
+        *out++ = static_cast<uint8_t>(acc >> held);
+    }
+    if (held) *out = static_cast<uint8_t>(acc << (8 - held));
 }
 
 }  // namespace
@@ -67,14 +134,9 @@ Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const
     const uint32_t pad = static_cast<uint32_t>(out % V);
     f.lane_stride = static_cast<uint32_t>(align16(pad + numel));
     f.lanes.assign(static_cast<size_t>(es - 1) * f.lane_stride, 0);
-    std::vector<uint8_t> sym(numel);
-    for (uint32_t i = 0; i < numel; ++i) {
-        uint32_t v = load_word(src + static_cast<size_t>(i) * es, es);
-        if (spec.bit_reorder) v = reorder_forward(v, spec.mantissa_bits, spec.exponent_bits);
-        sym[i] = static_cast<uint8_t>(v >> (8 * (es - 1)));
-        for (unsigned k = 0; k + 1 < es; ++k)
-            f.lanes[static_cast<size_t>(k) * f.lane_stride + pad + i] = static_cast<uint8_t>(v >> (8 * k));
-    }
+    thread_local std::vector<uint8_t> sym;
+    sym.resize(numel);
+    split_lanes(src, numel, spec, sym.data(), f.lanes.data() + pad, f.lane_stride);
     if (!book) {
         f.kind = NZ_KIND_RAW;
         f.bits.assign(f.lane_stride, 0);
@@ -87,66 +149,56 @@ Fragment encode_fragment(const uint8_t* src, uint32_t numel, uint64_t out, const
         return f;
     }
     f.kind = book->longest > 32 ? NZ_KIND_LONG : NZ_KIND_SHORT;
-    // greedy pair parse (gpu_layout.h:232-239, mixed_huffman.h:85-94)
-    std::vector<uint16_t> tokens;
-    tokens.reserve(numel);
+    // greedy pair parse (gpu_layout.h:232-239, mixed_huffman.h:85-94): a
+    // pair token only where index + 1 < numel
+    thread_local std::vector<uint16_t> tokens;
+    tokens.resize(numel);
+    size_t n_tokens = 0;
     uint64_t bit_length = 0;
+    const uint8_t* lengths = book->lengths.data();
+    const uint16_t* pair_token = book->pair_token.data();
     for (uint32_t i = 0; i < numel;) {
         unsigned token = sym[i];
         if (book->mixed && i + 1 < numel) {
-            const unsigned pair = book->pair_token[sym[i] | (static_cast<unsigned>(sym[i + 1]) << 8)];
+            const unsigned pair = pair_token[sym[i] | (static_cast<unsigned>(sym[i + 1]) << 8)];
             if (pair) token = pair;
         }
-        const unsigned length = book->lengths[token];
-        if (!length)
+        if (!lengths[token])
             fail(kUncodedSymbol, "Symbol " + std::to_string(token) + " at index " + std::to_string(i) +
                                      " has no codebook entry.");
-        tokens.push_back(static_cast<uint16_t>(token));
-        bit_length += length;
-        i += Codebook::token_width(token);
+        tokens[n_tokens++] = static_cast<uint16_t>(token);
+        bit_length += lengths[token];
+        i += token < 256 ? 1u : 2u;
     }
     f.bit_length = bit_length;
     const uint64_t n_windows = (bit_length + NZ_WINDOW_BITS - 1) / NZ_WINDOW_BITS;
     if (n_windows > 0xFFFFFFFFull) fail(kLayoutLimit, "Fragment bitstream too long.");
     f.n_windows = static_cast<uint32_t>(n_windows);
     f.bits.assign(8 * n_windows + NZ_BITS_PAD, 0);
-    {
-        uint64_t acc = 0;
-        unsigned pending = 0;
-        size_t cursor = 0;
-        for (uint16_t t : tokens) {
-            const unsigned len = book->lengths[t];
-            const uint64_t code = book->codes[t];
-            // append `len` bits, most significant first, flushing whole bytes
-            for (unsigned done = 0; done < len;) {
-                const unsigned take = std::min(len - done, 56u - pending);
-                const uint64_t part = (code >> (len - done - take)) & ((uint64_t(1) << take) - 1);
-                acc = (acc << take) | part;
-                pending += take;
-                done += take;
-                while (pending >= 8) {
-                    pending -= 8;
-                    f.bits[cursor++] = static_cast<uint8_t>(acc >> pending);
-                }
-                acc &= pending ? (uint64_t(1) << pending) - 1 : 0;
-            }
-        }
-        if (pending) f.bits[cursor++] = static_cast<uint8_t>(acc << (8 - pending));
-    }
+    pack_codes(tokens.data(), n_tokens, lengths, book->codes.data(), f.bits.data());
     // simulate the kernel's step sequence to place window boundaries
     f.meta.resize(n_windows);
-    std::vector<uint32_t> counts(n_windows);
+    thread_local std::vector<uint32_t> counts;
+    counts.assign(n_windows, 0);
     uint64_t pos = 0, total = 0;
+    const uint32_t* primary = book->lut.data() + NZ_LUT_HEADER;
     for (uint64_t w = 0; w < n_windows; ++w) {
         const uint64_t gap = pos - w * NZ_WINDOW_BITS;
         if (gap > 255) fail(kLayoutLimit, "Window gap exceeds its byte.");
         const uint64_t end = std::min<uint64_t>((w + 1) * NZ_WINDOW_BITS, bit_length);
         uint32_t count = 0;
         while (pos < end) {
-            uint32_t bytes;
-            unsigned n;
-            pos += lut_step(book->lut, peek64(f.bits.data(), pos), &bytes, &n);
-            count += n;
+            const uint64_t window = peek64(f.bits.data(), pos);
+            const uint32_t e = primary[2 * (window >> (64 - NZ_LUT_BITS))];
+            if (e >> NZ_ENTRY_COUNT) {   // whole tokens inside the 12-bit prefix
+                count += e >> NZ_ENTRY_COUNT;
+                pos += 32u - (e & NZ_ENTRY_SHIFT_MASK);
+            } else {                     // a longer code: the checked escape search
+                uint32_t bytes;
+                unsigned n;
+                pos += lut_step(book->lut, window, &bytes, &n);
+                count += n;
+            }
         }
         if (count > 255) fail(kLayoutLimit, "Window count exceeds its byte.");
         f.meta[w] = static_cast<uint16_t>(gap | (count << 8));

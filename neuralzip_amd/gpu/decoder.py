@@ -120,9 +120,11 @@ class HIPDecoder:
         _native.lib()
         return group.layout
 
-    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), slots=SLOTS):
+    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), slots=SLOTS, cached_stores=False):
         """Tiles of `fragment_indices` (one dtype and kind), ordered so that
-        fragments of one LUT are adjacent, and their launch plan."""
+        fragments of one LUT are adjacent, and their launch plan. With
+        `cached_stores` the launch writes with ordinary stores, for a
+        consumer that reads the words right after the decode."""
         fragment_indices = list(fragment_indices)
         if not fragment_indices:
             raise ValueError("A decode batch must contain at least one group.")
@@ -141,7 +143,8 @@ class HIPDecoder:
         tiles_t = torch.from_numpy(tiles.view(np.uint8).copy()).to(device)
         segments_t = torch.from_numpy(segments.view(np.uint8).copy()).to(device)
         args = (store.buffer.data_ptr(), store.frags.data_ptr(), tiles_t.data_ptr(), segments_t.data_ptr(),
-                len(segments), key[0], int(key[1]), int(key[2]), output.data_ptr())
+                len(segments), key[0], int(key[1]), int(key[2]), output.data_ptr(),
+                _native.DECODE_CACHED_STORES if cached_stores else 0)
         return PreparedBatch((tiles_t, segments_t), device, key, (len(segments),), len(segments), store, output,
                              tuple(outputs), algorithmic_bytes(store.descs[fragment_indices], dtype), args)
 
@@ -259,7 +262,8 @@ class HIPDecoder:
         batch holds its device arrays, so the saved pointers stay valid."""
         if stream is None:
             stream = torch.cuda.current_stream(prepared.device)
-        _native.decode_launch(*prepared.launch_args, stream.cuda_stream)
+        *args, flags = prepared.launch_args
+        _native.decode_launch(*args, stream.cuda_stream, flags)
         return prepared.outputs
 
 

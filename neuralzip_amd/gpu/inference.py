@@ -11,6 +11,7 @@ also launches the decode of block N+1 on a side stream into the other
 workspace slot, ordered after everything already queued on the compute
 stream (which includes the last reads of that slot, by block N-1).
 """
+import contextlib
 from collections import defaultdict
 from dataclasses import dataclass, field
 from functools import cached_property, partial
@@ -28,6 +29,9 @@ from neuralzip_amd.gpu import decoder as gpu_decoder
 from neuralzip_amd.utils import _stream_chunk_size, tensor_words
 
 RUNTIME_ATTRIBUTE = "neuralzip_runtime"
+# Decode units of the runtime: whole hook blocks (the reference's), or single
+# weights decoded right before their own forward.
+GRANULARITIES = ("block", "linear")
 _GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
 # Tensor offsets in a workspace: 128 elements keeps views 256-byte aligned
 # and fragment starts 16-element aligned (the layout's vector alignment).
@@ -400,48 +404,69 @@ class NeuralZipRuntime:
     reference, which always decodes.
     """
 
-    def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0, decode_slots=None):
+    def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0, decode_slots=None,
+                 granularity="block"):
+        if granularity not in GRANULARITIES:
+            raise ValueError(f"granularity must be one of {GRANULARITIES}.")
+        if granularity == "linear" and matvec_tokens:
+            raise ValueError("Fused products run per block; use granularity='block' with matvec_tokens.")
         self.model = model
         self.export = exported
         self.device = torch.device(device)
-        self.prefetch = bool(prefetch)
+        self.granularity = granularity
+        # one weight at a time, decoded inline right before its own forward:
+        # nothing to prefetch into
+        self.prefetch = bool(prefetch) and granularity == "block"
         self.decode_slots = decode_slots   # workgroups per decode launch; None: one per CU
         self.matvec_tokens = int(matvec_tokens)
         if not 0 <= self.matvec_tokens <= _native.MATVEC_MAX_BATCH:
             raise ValueError(f"matvec_tokens must be in [0, {_native.MATVEC_MAX_BATCH}].")
         self._decoder = gpu_decoder.default_decoder()
         self._hook_handles = []
-        order = exported.block_order
-        # block -> the block whose decode its hook prefetches (the first after the last)
+        # decode units: blocks, or single weights; each exported tensor's unit
+        # and its element offset inside the unit
+        by_key = {(g.block_name, g.encoded.dtype.torch_dtype, b.workspace_offset): b
+                  for g in exported.groups for b in g.bindings}
+        entries = []
+        for layout, ids, offset, config, block in exported.tensors:
+            binding = by_key[(block, config.torch_dtype, offset)]
+            unit, inner = (block, offset) if granularity == "block" else (binding.tensor_name, 0)
+            entries.append((unit, inner, layout, ids, config, binding))
+        order = tuple(dict.fromkeys(unit for unit, *_ in entries))
+        self.units = order
+        # unit -> the unit whose decode its hook prefetches (the first after the last)
         self._following = {name: order[(i + 1) % len(order)] for i, name in enumerate(order)}
         n_slots = 1 if not self.prefetch or len(order) < 2 else (2 if len(order) % 2 == 0 else 3)
         self.block_slot = {name: (i % 2 if n_slots > 1 else 0) for i, name in enumerate(order)}
         if n_slots == 3:
             self.block_slot[order[-1]] = 2
-        block_sizes = defaultdict(int)
-        for group in exported.groups:
-            key = (group.encoded.dtype.torch_dtype, self.block_slot[group.block_name])
-            block_sizes[key] = max(block_sizes[key], _align(group.workspace_offset + group.encoded.numel))
+        unit_sizes = defaultdict(int)
+        for unit, inner, layout, ids, config, binding in entries:
+            key = (config.torch_dtype, self.block_slot[unit])
+            unit_sizes[key] = max(unit_sizes[key], _align(inner + binding.numel))
         self.slot_offsets, self.workspaces = {}, {}
-        for dtype in {d for d, _ in block_sizes}:
+        for dtype in {d for d, _ in unit_sizes}:
             cursor = 0
             for slot in range(n_slots):
                 self.slot_offsets[(dtype, slot)] = cursor
-                cursor += _align(block_sizes.get((dtype, slot), 0))
+                cursor += _align(unit_sizes.get((dtype, slot), 0))
             self.workspaces[dtype] = torch.empty(max(cursor, 1), dtype=dtype, device=self.device)
-        # the packed device store: every tensor at its slot's offset
-        tensors, by_block, frag_base, tensor_frags = [], defaultdict(list), 0, {}
-        for layout, ids, offset, config, name in exported.tensors:
-            slot_base = self.slot_offsets[(config.torch_dtype, self.block_slot[name])]
-            tensors.append((layout, ids, slot_base + offset))
+        # the packed device store: every tensor at its unit's slot offset
+        tensors, by_unit, frag_base, tensor_frags = [], defaultdict(list), 0, {}
+        self._binding_offset, self._unit_bindings = {}, defaultdict(list)
+        for unit, inner, layout, ids, config, binding in entries:
+            base = self.slot_offsets[(config.torch_dtype, self.block_slot[unit])] + inner
+            tensors.append((layout, ids, base))
             frags = range(frag_base, frag_base + layout.n_fragments)
-            by_block[(name, config.torch_dtype)].extend(frags)
-            tensor_frags[(name, config.torch_dtype, offset)] = frags
+            by_unit[(unit, config.torch_dtype)].extend(frags)
+            tensor_frags[(binding.module_name, config.torch_dtype)] = frags
+            self._binding_offset[binding] = base
+            self._unit_bindings[unit].append((config.torch_dtype, binding))
             frag_base += layout.n_fragments
         self.store = gpu_decoder.DeviceStore(exported.codebooks, tensors, self.device)
         self._prepared_batches = defaultdict(list)
         self.algorithmic_bytes = {}
-        for (name, dtype), frags in by_block.items():
+        for (name, dtype), frags in by_unit.items():
             spec = DTYPES[dtype]
             kinds = defaultdict(list)
             for f in frags:
@@ -455,7 +480,10 @@ class NeuralZipRuntime:
                     resident = self._decoder.slots(self.device, (spec.element_size, bool(spec.bit_reorder),
                                                                  bool(long_codes)))
                     slots = max(1, min(resident, self._compute_units()))
-                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype], slots=slots)
+                # a weight decoded right before its own GEMM is read back at
+                # once: ordinary stores leave it in the caches for that read
+                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype], slots=slots,
+                                                    cached_stores=granularity == "linear")
                 self._prepared_batches[name].append(batch)
                 self.algorithmic_bytes[name] = self.algorithmic_bytes.get(name, 0) + batch.algorithmic_bytes
         self._groups_by_block = defaultdict(list)
@@ -464,7 +492,8 @@ class NeuralZipRuntime:
         self.side_stream = torch.cuda.Stream(self.device) if self.prefetch else None
         with torch.cuda.device(self.device):
             self._events = {name: (torch.cuda.Event(), torch.cuda.Event()) for name in order} if self.prefetch else {}
-        self._pending = None   # (block name, event) decoded ahead on the side stream
+        self._pending = None   # (unit name, event) decoded ahead on the side stream
+        self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
         self._matvec, self._matvec_blocks, self._partials = {}, frozenset(), None
         self._fused = set()    # blocks whose current call runs the fused products
         if self.matvec_tokens:
@@ -484,8 +513,8 @@ class NeuralZipRuntime:
                     block_plans = None
                     break
                 rows, cols = binding.shape
-                offset = self.slot_offsets[(spec.torch_dtype, self.block_slot[name])] + binding.workspace_offset
-                member = (tensor_frags[(name, spec.torch_dtype, binding.workspace_offset)], offset, rows)
+                offset = self._binding_offset[binding]
+                member = (tensor_frags[(binding.module_name, spec.torch_dtype)], offset, rows)
                 try:
                     block_plans[binding.module_name] = self._decoder.prepare_matvec(self.store, [member], spec, cols)
                 except _native.NativeError:
@@ -564,7 +593,8 @@ class NeuralZipRuntime:
         return ys[names.index(module_name)]
 
     @classmethod
-    def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0, decode_slots=None):
+    def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0, decode_slots=None,
+               granularity="block"):
         if hasattr(model, RUNTIME_ATTRIBUTE):
             raise RuntimeError("This model already has a NeuralZip runtime.")
         if not exported.groups:
@@ -580,29 +610,52 @@ class NeuralZipRuntime:
         decoder = gpu_decoder.default_decoder()
         for group in exported.groups:
             decoder.prepare_group(device.index, group)
+        grad_flags = {}
         for binding in exported.bindings:
             module = _binding_module(model, binding)
+            grad_flags[binding] = bool(getattr(module.weight, "requires_grad", False))
             module._parameters.pop("weight", None)
             module.__dict__.pop("weight", None)
         model.to(device).eval()
         runtime = cls(model, exported, device, prefetch=prefetch, matvec_tokens=matvec_tokens,
-                      decode_slots=decode_slots)
+                      decode_slots=decode_slots, granularity=granularity)
+        runtime._grad_flags = grad_flags
         runtime._install()
         return runtime
 
     def _binding_view(self, dtype, block_name, binding):
-        base = self.slot_offsets[(dtype, self.block_slot[block_name])] + binding.workspace_offset
+        base = self._binding_offset[binding]
         return self.workspaces[dtype][base:base + binding.numel].view(binding.shape)
 
+    def _unit_hook_module(self, unit):
+        """The module whose forward pre-hook decodes `unit`: the block's hook
+        module, or for one weight its own module, except a MultiheadAttention's
+        out_proj, whose weight the attention reads without calling it."""
+        if self.granularity == "block":
+            return _hook_module(self.model, self.export, unit)
+        (_, binding), = self._unit_bindings[unit]
+        parent_name, _, attribute = binding.module_name.rpartition(".")
+        parent = self.model.get_submodule(parent_name)
+        if attribute == "out_proj" and isinstance(parent, nn.MultiheadAttention):
+            return parent
+        return self.model.get_submodule(binding.module_name)
+
     def _install(self):
-        for name, groups in self._groups_by_block.items():
-            for group in groups:
-                for binding in group.bindings:
-                    _binding_module(self.model, binding).__dict__["weight"] = self._binding_view(
-                        group.encoded.dtype.torch_dtype, name, binding)
-        for name in self.export.block_order:
-            handle = _hook_module(self.model, self.export, name).register_forward_pre_hook(
-                partial(self._decode_block, name), prepend=True, with_kwargs=True)
+        # The injected weight keeps the original parameter's requires_grad
+        # flag: torch's matmul folds a strided 3-D input into one matrix
+        # product only for a weight that requires grad, and runs a batched
+        # product (other rounding) otherwise, so the flag decides which GEMM
+        # computes, e.g., the lm_head of a sliced batch.
+        flags = getattr(self, "_grad_flags", {})
+        for unit in self.units:
+            for dtype, binding in self._unit_bindings[unit]:
+                view = self._binding_view(dtype, unit, binding)
+                if flags.get(binding, False):
+                    view = nn.Parameter(view, requires_grad=True)
+                _binding_module(self.model, binding).__dict__["weight"] = view
+        for unit in self.units:
+            handle = self._unit_hook_module(unit).register_forward_pre_hook(
+                partial(self._decode_block, unit), prepend=True, with_kwargs=True)
             self._hook_handles.append(handle)
         blocks = {b.module_name: g.block_name for g in self.export.groups for b in g.bindings}
         for module_name in self._matvec:
@@ -656,7 +709,7 @@ class NeuralZipRuntime:
         if self.side_stream is None:
             return
         following = self._following[block_name]
-        if following == block_name:
+        if following == block_name or (not self._wrap and following == self.units[0]):
             return
         # everything queued so far (the last readers of `following`'s slot
         # included) completes before the side stream overwrites that slot;
@@ -674,19 +727,31 @@ class NeuralZipRuntime:
             torch.cuda.current_stream(self.device).wait_event(self._pending[1])
             self._pending = None
 
+    @contextlib.contextmanager
+    def graph_capture(self):
+        """Wrap the capture of whole forwards into a HIP graph (torch.cuda.graph):
+        no side-stream decode is pending from before the capture or left
+        pending after it, and the last block does not prefetch the first
+        (each replay decodes it at its start)."""
+        self.drain()
+        self._wrap = False
+        try:
+            yield self
+        finally:
+            self.drain()
+            self._wrap = True
+
     @torch.no_grad()
     def materialized_weights(self):
-        """Yield compressed weights as bit-exact CPU tensors, one block at a time."""
+        """Yield compressed weights as bit-exact CPU tensors, one decode unit at a time."""
         self.drain()
         yielded = set()
         current = torch.cuda.current_stream(self.device)
-        for name in self.export.block_order:
-            self._launch(name, current)
+        for unit in self.units:
+            self._launch(unit, current)
             torch.cuda.synchronize(self.device)
-            for group in self._groups_by_block[name]:
-                for binding in group.bindings:
-                    if binding.tensor_name in yielded:
-                        continue
-                    yielded.add(binding.tensor_name)
-                    view = self._binding_view(group.encoded.dtype.torch_dtype, name, binding)
-                    yield binding.tensor_name, view.detach().to("cpu", copy=True)
+            for dtype, binding in self._unit_bindings[unit]:
+                if binding.tensor_name in yielded:
+                    continue
+                yielded.add(binding.tensor_name)
+                yield binding.tensor_name, self._binding_view(dtype, unit, binding).detach().to("cpu", copy=True)

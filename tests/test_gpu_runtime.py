@@ -127,3 +127,90 @@ def test_block_launch_workgroups(decode_slots):
                 assert min(cus, resident) < batch.n_segments <= decode_slots
     for _ in range(3):
         assert exact(model.blocks[1](model.blocks[0](x)), expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_linear_granularity_decodes_each_weight_before_its_forward(dtype):
+    """granularity='linear': one scratch slot per dtype holds whichever
+    weight runs next; each weight is decoded (cached stores) by its own
+    module's pre-hook. Outputs and materialized weights stay bitwise equal,
+    also with a raw fragment and after poisoning the slot."""
+    torch.manual_seed(42)
+    model = Model(dtype).eval()
+    pattern(model, dtype)
+    named = {name: p.detach().clone() for name, p in model.named_parameters()}
+    setup = NeuralZipSetup(chunk_size=8192).build(named)
+    key = next(iter(setup.chunk_codebooks))
+    ids = list(setup.chunk_codebooks[key])
+    ids[len(ids) // 2] = None
+    setup.chunk_codebooks[key] = tuple(ids)
+    baseline = copy.deepcopy(model).cuda()
+    inputs = torch.ones(3, 257, dtype=dtype, device="cuda")
+    expected = baseline(inputs).cpu()
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0",
+                                      granularity="linear")
+    assert runtime.units == ("layers.0.weight", "layers.1.weight") and not runtime.prefetch
+    # both weights are views of the same slot
+    w0, w1 = model.layers[0].weight, model.layers[1].weight
+    assert w0.data_ptr() == w1.data_ptr() == runtime.workspaces[dtype].data_ptr()
+    assert all(b.launch_args[-1] == 1 for batches in runtime._prepared_batches.values() for b in batches)
+    restored = dict(runtime.materialized_weights())
+    assert all(exact(restored[name], t) for name, t in named.items())
+    for _ in range(3):
+        runtime.workspaces[dtype].view(torch.uint8).fill_(0xA5)
+        assert exact(model(inputs), expected)
+
+
+def test_linear_granularity_multihead_attention_out_proj():
+    """MultiheadAttention reads out_proj.weight without calling out_proj:
+    with per-weight decoding, that weight is decoded by the attention's hook."""
+    torch.manual_seed(3)
+    model = nn.Module()
+    model.attn = nn.MultiheadAttention(256, 4, dtype=torch.bfloat16)
+    model.proj = nn.Linear(256, 256, dtype=torch.bfloat16)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape) * 0.02)
+    reference = copy.deepcopy(model).cuda().eval()
+    x = torch.randn(5, 2, 256, dtype=torch.bfloat16, device="cuda")
+
+    def forward(m):
+        return m.proj(m.attn(x, x, x, need_weights=False)[0])
+    with torch.no_grad():
+        expected = forward(reference)
+    setup = NeuralZipSetup(chunk_size=16384).build({n: p.detach() for n, p in model.named_parameters()})
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0",
+                                      granularity="linear")
+    assert "attn.out_proj.weight" in runtime.units
+    assert runtime._unit_hook_module("attn.out_proj.weight") is model.attn
+    for _ in range(3):
+        runtime.workspaces[torch.bfloat16].view(torch.uint8).fill_(0xA5)
+        with torch.no_grad():
+            assert exact(forward(model), expected)
+
+
+@pytest.mark.parametrize("granularity", ["block", "linear"])
+def test_injected_weights_keep_the_original_gemm_path(granularity):
+    """A Linear applied to a strided 3-D slice (as lm_head is under
+    logits_to_keep at batch > 1): torch's matmul folds it into one matrix
+    product only when the weight requires grad, and runs a batched product
+    (other rounding) otherwise. The injected weight keeps the original
+    parameter's requires_grad, so the result is the uncompressed model's,
+    bit for bit."""
+    torch.manual_seed(5)
+    model = nn.Module()
+    model.layers = nn.ModuleList([nn.Linear(4096, 16384, bias=False, dtype=torch.bfloat16)])
+    with torch.no_grad():
+        model.layers[0].weight.copy_(torch.randn(16384, 4096) * 0.02)
+    reference = copy.deepcopy(model).cuda()
+    hidden = torch.randn(32, 128, 4096, dtype=torch.bfloat16, device="cuda")
+    x = hidden[:, -16:, :]
+    with torch.no_grad():
+        expected = reference.layers[0](x)
+    setup = NeuralZipSetup().build({n: p.detach() for n, p in model.named_parameters()})
+    NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", granularity=granularity)
+    weight = model.layers[0].weight
+    assert isinstance(weight, nn.Parameter) and weight.requires_grad
+    assert "weight" not in model.layers[0]._parameters
+    with torch.no_grad():
+        assert exact(model.layers[0](x), expected)

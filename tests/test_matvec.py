@@ -217,12 +217,10 @@ def test_matvec_long_codes():
     check_product(first, w, x, None, torch.bfloat16)
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_grouped_product_equals_separate_products(dtype):
-    """Three weights sharing x in one launch (rows stacked in workspace order,
-    a raw chunk and two codebooks among them) give each weight the bits of
-    its own launch."""
+def grouped_case(dtype):
+    """Three weights sharing x (rows stacked in workspace order, a raw chunk
+    and two codebooks among them): (weights, base, descs, tiles, x, biases,
+    [(offset, rows)], fragment step)."""
     cols = 4096
     shapes = [(40, cols), (8, cols), (24, cols)]
     ws = [random_weight(dtype, r, c, seed=10 + i) for i, (r, c) in enumerate(shapes)]
@@ -246,6 +244,16 @@ def test_grouped_product_equals_separate_products(dtype):
     x = torch.randn(2, cols, generator=g).to(dtype)
     biases = [(torch.randn(r, generator=g) * 0.1).to(dtype) if i != 1 else None for i, (r, _) in enumerate(shapes)]
     weights = [(off, w.shape[0]) for off, w in zip(offsets, ws)]
+    return ws, base, descs, tiles, x, biases, weights, step
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_product_equals_separate_products(dtype):
+    """Three weights sharing x in one launch give each weight the bits of
+    its own launch."""
+    ws, base, descs, tiles, x, biases, weights, step = grouped_case(dtype)
+    cols = x.shape[1]
     (grouped,) = run_matvec(base, descs, tiles, dtype, weights, cols, x, biases, calls=1)
     frag_of = np.repeat(np.arange(len(ws)), [-(-w.numel() // step) for w in ws])
     for i, (w, b) in enumerate(zip(ws, biases)):
