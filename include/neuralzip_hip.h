@@ -241,6 +241,27 @@ int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const n
                      uint32_t n_weights, const float* partials, uint32_t batch, int element_size, int bit_reorder,
                      void* stream);
 
+/* Bytes of partial sums the no-allocation product holds per GPU. */
+#define NZ_MATVEC_SCRATCH_BYTES (32u << 20)
+
+/* Both passes of a fused product in one call that allocates nothing: the
+ * launches of nz_matvec_launch (short_segments, then long_segments, either
+ * count may be 0) and nz_matvec_reduce, with the partial sums in a
+ * library-owned device array of NZ_MATVEC_SCRATCH_BYTES per GPU instead of
+ * a caller buffer; row_index / entries / weights[k].y / bias as for
+ * nz_matvec_reduce. A product needing more than the array
+ * (2 * n_tiles * batch * 4 bytes) fails with NZ_LAYOUT_LIMIT. Every call on
+ * one GPU uses that GPU's array: calls that overlap on a GPU (on different
+ * streams) race; each call writes every partial it reads, so none needs
+ * clearing. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Asynchronous on `stream`. */
+int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                      const nz_work* short_segments, uint32_t n_short, const nz_work* long_segments,
+                      uint32_t n_long, int element_size, int bit_reorder, const nz_matvec_weight* weights,
+                      uint32_t n_weights, uint32_t cols, const void* x, uint32_t batch, const uint32_t* row_index,
+                      const uint32_t* entries, void* stream);
+
 /* ---- storage format (host codecs) -------------------------------------- */
 
 /* Huff0 tree description for a 256-bin histogram plus `prior_count` per

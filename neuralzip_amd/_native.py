@@ -70,6 +70,8 @@ ABI_VERSION = 6
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
 MATVEC_MAX_WEIGHTS = 4
+# Partial-sum bytes of the no-allocation product (NZ_MATVEC_SCRATCH_BYTES).
+MATVEC_SCRATCH_BYTES = 32 << 20
 
 
 def lib():
@@ -104,6 +106,8 @@ def lib():
         L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, u32,
                                        vp, u32, vp, u32, vp]
         L.nz_matvec_reduce.argtypes = [vp, vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp]
+        L.nz_matvec_noalloc.argtypes = [vp, vp, vp, u32, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp, u32, u32,
+                                        vp, u32, vp, vp, vp]
         L.nz_chunk_histograms.argtypes = [vp, u64, ctypes.POINTER(_LaneLayout), u64, ctypes.c_int, vp, vp]
         L.nz_clusterer_create.argtypes = [ctypes.c_double, ctypes.c_int, ctypes.POINTER(vp)]
         L.nz_clusterer_destroy.argtypes = [vp]
@@ -303,6 +307,18 @@ def matvec_reduce(row_index_ptr, entries_ptr, weights, partials_ptr, batch, elem
     """`weights`: a MatvecWeight array whose y (and bias) pointers are set."""
     check(lib().nz_matvec_reduce(row_index_ptr, entries_ptr, ctypes.cast(weights, ctypes.c_void_p), len(weights),
                                  partials_ptr, int(batch), int(element_size), int(bit_reorder), stream_ptr))
+
+
+def matvec_noalloc(base_ptr, frags_ptr, tiles_ptr, n_tiles, short_ptr, n_short, long_ptr, n_long, element_size,
+                   bit_reorder, weights, cols, x_ptr, batch, row_index_ptr, entries_ptr, stream_ptr):
+    """Both passes of a fused product with the partial sums in the library's
+    own per-device array (no allocation; 2 * n_tiles * batch * 4 bytes at
+    most MATVEC_SCRATCH_BYTES). `weights`: a MatvecWeight array with y (and
+    bias) set. Calls that overlap on one GPU share the array and race."""
+    check(lib().nz_matvec_noalloc(base_ptr, frags_ptr, tiles_ptr, int(n_tiles), short_ptr, int(n_short), long_ptr,
+                                  int(n_long), int(element_size), int(bit_reorder),
+                                  ctypes.cast(weights, ctypes.c_void_p), len(weights), int(cols), x_ptr, int(batch),
+                                  row_index_ptr, entries_ptr, stream_ptr))
 
 
 def chunk_histograms(words, spec, chunk_elements, *, threads=0, lane_counts=True):

@@ -45,6 +45,12 @@ extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const v
                                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
                                     uint32_t batch, float* partials, uint32_t n_tiles, void* stream, char* message,
                                     size_t message_size);
+extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const void* tiles, uint32_t n_tiles,
+                                     const void* short_segs, uint32_t n_short, const void* long_segs,
+                                     uint32_t n_long, int element_size, int bit_reorder,
+                                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols,
+                                     const void* x, uint32_t batch, const uint32_t* row_index,
+                                     const uint32_t* entries, void* stream, char* message, size_t message_size);
 extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
                                     uint32_t n_weights, const float* partials, uint32_t batch, int element_size,
                                     int bit_reorder, void* stream, char* message, size_t message_size);
@@ -288,6 +294,32 @@ int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const n
     char message[256] = {0};
     const int rc = nz_hip_matvec_reduce(row_index, entries, weights, n_weights, partials, batch, element_size,
                                         bit_reorder, stream, message, sizeof message);
+    if (rc) return set_error(rc, message);
+    return 0;
+}
+
+int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+                      const nz_work* short_segments, uint32_t n_short, const nz_work* long_segments,
+                      uint32_t n_long, int element_size, int bit_reorder, const nz_matvec_weight* weights,
+                      uint32_t n_weights, uint32_t cols, const void* x, uint32_t batch, const uint32_t* row_index,
+                      const uint32_t* entries, void* stream) {
+    if (!base || !frags || !tiles || !x || !weights || !row_index || !entries || (n_short && !short_segments) ||
+        (n_long && !long_segments))
+        return set_error(nz::kInvalidArgument, "Null matvec argument.");
+    const int rc0 = guarded([&] {
+        if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
+        nz::check_matvec_group(weights, n_weights, cols, static_cast<unsigned>(element_size));
+        if (batch == 0 || batch > NZ_MATVEC_MAX_BATCH) nz::fail(nz::kInvalidArgument, "matvec batch must be in [1, 4].");
+        if (static_cast<uint64_t>(batch) * cols * static_cast<uint64_t>(element_size) > 0xFFFFFFFFull)
+            nz::fail(nz::kInvalidArgument, "Activation rows exceed the addressable range.");
+        for (uint32_t k = 0; k < n_weights; ++k)
+            if (!weights[k].y) nz::fail(nz::kInvalidArgument, "Null matvec output.");
+    });
+    if (rc0) return rc0;
+    char message[256] = {0};
+    const int rc = nz_hip_matvec_noalloc(base, frags, tiles, n_tiles, short_segments, n_short, long_segments, n_long,
+                                         element_size, bit_reorder, weights, n_weights, cols, x, batch, row_index,
+                                         entries, stream, message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }

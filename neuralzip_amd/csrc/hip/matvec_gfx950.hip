@@ -25,6 +25,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../nz_format.h"
 #include "neuralzip_hip.h"
 #include "tile_decode.h"
@@ -547,4 +549,75 @@ extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* e
         return -6;
     }
     return 0;
+}
+
+// ---- the entry point that allocates nothing ------------------------------
+
+// Partial sums of nz_matvec_noalloc: one array per GPU (each device holds its
+// own copy, from the library's first kernel launch on it until the process
+// ends). Host code never names it in a kernel argument: the array's name is a
+// host-side stand-in there, so its device address is looked up per device.
+static __device__ __align__(256) float scratch[NZ_MATVEC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+float* g_scratch[kMaxDevices] = {};
+
+// The current device's address of `scratch`, from hipGetSymbolAddress with
+// that device current, once per device.
+hipError_t scratch_address(float** out) {
+    int device = 0;
+    hipError_t rc = hipGetDevice(&device);
+    if (rc != hipSuccess) return rc;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> hold(g_scratch_lock);
+    if (g_scratch[device] == nullptr) {
+        void* address = nullptr;
+        rc = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (rc != hipSuccess) return rc;
+        g_scratch[device] = static_cast<float*>(address);
+    }
+    *out = g_scratch[device];
+    return hipSuccess;
+}
+
+}  // namespace
+
+// Both passes of a fused product (nz_hip_matvec_launch per codebook kind,
+// then nz_hip_matvec_reduce) with the partial sums in `scratch`. Every
+// partial the reduce reads is written by this call's first pass, so nothing
+// needs clearing; calls that overlap on one GPU share the array and race.
+extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const void* tiles, uint32_t n_tiles,
+                                     const void* short_segs, uint32_t n_short, const void* long_segs,
+                                     uint32_t n_long, int element_size, int bit_reorder,
+                                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols,
+                                     const void* x, uint32_t batch, const uint32_t* row_index,
+                                     const uint32_t* entries, void* stream, char* message, size_t message_size) {
+    const uint64_t need = 2ull * n_tiles * batch * sizeof(float);
+    if (need > NZ_MATVEC_SCRATCH_BYTES) {
+        snprintf(message, message_size,
+                 "The product needs %llu bytes of partial sums; the no-allocation entry point holds %u "
+                 "(use nz_matvec_launch with a caller buffer).",
+                 static_cast<unsigned long long>(need), NZ_MATVEC_SCRATCH_BYTES);
+        return -4;
+    }
+    float* partials = nullptr;
+    const hipError_t found = scratch_address(&partials);
+    if (found != hipSuccess) {
+        snprintf(message, message_size, "scratch lookup failed: %s", hipGetErrorString(found));
+        return -6;
+    }
+    int rc = 0;
+    if (n_short)
+        rc = nz_hip_matvec_launch(base, frags, tiles, short_segs, n_short, element_size, bit_reorder, 0, weights,
+                                  n_weights, cols, x, batch, partials, n_tiles, stream, message, message_size);
+    if (rc == 0 && n_long)
+        rc = nz_hip_matvec_launch(base, frags, tiles, long_segs, n_long, element_size, bit_reorder, 1, weights,
+                                  n_weights, cols, x, batch, partials, n_tiles, stream, message, message_size);
+    if (rc == 0)
+        rc = nz_hip_matvec_reduce(row_index, entries, weights, n_weights, partials, batch, element_size, bit_reorder,
+                                  stream, message, message_size);
+    return rc;
 }

@@ -6,6 +6,7 @@ import re
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from neuralzip_amd import _native
@@ -83,3 +84,20 @@ def test_matvec_weight_layout_matches_the_bindings(tmp_path):
     W = _native.MatvecWeight
     assert values == [ctypes.sizeof(W), W.rows.offset, W.y.offset, W.bias.offset, W.offset.offset,
                       _native.MATVEC_MAX_BATCH, _native.MATVEC_MAX_WEIGHTS]
+
+
+def test_no_alloc_product_refuses_more_partials_than_its_array():
+    """nz_matvec_noalloc checks the product's partial sums against its fixed
+    array before touching the device: 2 * n_tiles * batch * 4 bytes over
+    NZ_MATVEC_SCRATCH_BYTES fails with NZ_LAYOUT_LIMIT (host-only call)."""
+    header = HEADER.read_text()
+    limit = int(eval(re.search(r"#define NZ_MATVEC_SCRATCH_BYTES \((.+?)\)", header).group(1).replace("u", "")))
+    assert limit == _native.MATVEC_SCRATCH_BYTES
+    lib = _native.lib()
+    weights = _native.matvec_weights([(0, 8, 1, None)])   # output pointer: never used, the call returns first
+    dummy = np.zeros(64, dtype=np.uint8)
+    too_many_tiles = limit // (2 * 4 * 4) + 1
+    rc = lib.nz_matvec_noalloc(dummy.ctypes.data, dummy.ctypes.data, dummy.ctypes.data, too_many_tiles,
+                               dummy.ctypes.data, 1, None, 0, 2, 1, ctypes.addressof(weights), 1, 2048,
+                               dummy.ctypes.data, 4, dummy.ctypes.data, dummy.ctypes.data, None)
+    assert rc == -4 and b"no-allocation" in lib.nz_last_error()
