@@ -16,6 +16,7 @@ the side stream) and generates again. Asserted:
     equal the original words.
 """
 import gc
+import resource
 import sys
 import time
 from pathlib import Path
@@ -32,7 +33,9 @@ DEVICE = torch.device("cuda:0")
 
 
 def log(message):
-    print(f"[models] {message}", flush=True)
+    peak = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 2 ** 20
+    print(f"[models] {message} (host peak {peak:.1f} GiB, GPU {torch.cuda.max_memory_allocated() / 2 ** 30:.0f} GiB)",
+          flush=True)
 
 
 def word_checksums(tensor, span=1 << 26):
