@@ -11,8 +11,13 @@ Prints one JSON line: value = decoded GB/s (bytes written / time of `steps`
 whole steps run back to back between two HIP events on the launch stream),
 plus the roofline of the dominant decode kernel (algorithmic bytes per
 launch / its mean duration over `steps` back-to-back launches, timed the same
-way) and a CPU baseline (the oracle's threaded storage decode of the same
-tensors on this host).
+way), a CPU baseline (the oracle's threaded storage decode of the same
+tensors on this host) and, under "model", the tok/s half of the metric: a
+Llama-3-8B-shaped model (random bf16 weights) generating greedily at batch 1
+uncompressed and through the NeuralZip runtime, eager and with each decode
+step replayed from a HIP graph, logits and tokens compared bit for bit. The
+model part runs first (about a minute), which also brings the device's
+clocks up before the kernel is timed.
 """
 import argparse
 import contextlib
@@ -247,6 +252,9 @@ def graph_generate(model, ids, new_tokens, runtime=None):
             out = step()
         torch.cuda.synchronize(device)
         replays = new_tokens - 3
+        # a spin kernel on each side of the replays marks them in kernel traces
+        torch.cuda._sleep(1000)
+        torch.cuda.synchronize(device)
         t0 = time.perf_counter()
         for _ in range(replays):
             graph.replay()
@@ -255,6 +263,7 @@ def graph_generate(model, ids, new_tokens, runtime=None):
             position += 1
         torch.cuda.synchronize(device)
         seconds = time.perf_counter() - t0
+        torch.cuda._sleep(1000)
     del graph
     return seconds, replays, torch.cat(generated, dim=1)
 
@@ -370,7 +379,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                       "uncompressed_ms_per_step": round(base_graph[0] / base_graph[1] * 1e3, 3),
                       "replayed_steps": nz_graph[1],
                       "tokens_identical_to_uncompressed": bool(torch.equal(nz_graph[2].cpu(), base_graph[2].cpu())),
-                      "tokens_identical_to_eager": bool(torch.equal(base_graph[2].cpu(),
+                      "uncompressed_graph_tokens_identical_to_eager": bool(torch.equal(base_graph[2].cpu(),
                                                                     base_out[:, prompt:].cpu()))}
     line = {
         "metric": f"tok/s {kind} shape bs={batch} vs uncompressed {dtype_name}",
@@ -396,7 +405,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                    "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
-                   "prefetch": runtime.prefetch, "decode_slots": slots or "one per CU", **matvec_info},
+                   "prefetch": runtime.prefetch, "decode_slots": slots or "3/4 of the CUs (prefetch) or one per CU", **matvec_info},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "graph": graph_info,

@@ -417,7 +417,7 @@ class NeuralZipRuntime:
         # one weight at a time, decoded inline right before its own forward:
         # nothing to prefetch into
         self.prefetch = bool(prefetch) and granularity == "block"
-        self.decode_slots = decode_slots   # workgroups per decode launch; None: one per CU
+        self.decode_slots = decode_slots   # workgroups per decode launch; None: the runtime's choice
         self.matvec_tokens = int(matvec_tokens)
         if not 0 <= self.matvec_tokens <= _native.MATVEC_MAX_BATCH:
             raise ValueError(f"matvec_tokens must be in [0, {_native.MATVEC_MAX_BATCH}].")
@@ -474,12 +474,16 @@ class NeuralZipRuntime:
             for long_codes, members in sorted(kinds.items()):
                 slots = decode_slots
                 if slots is None:
-                    # One workgroup per CU. The side-stream decode then shares
-                    # every CU with the compute stream's kernels, and the end
-                    # of one block's launch overlaps the start of the next.
+                    # A decode that runs beside the compute stream's kernels
+                    # gets one workgroup on three CUs in four: its workgroups
+                    # hold half of a CU's LDS and wavefront slots, and kernels
+                    # of the compute stream that share a CU with one run
+                    # slower. A decode on the compute stream alone gets one
+                    # workgroup per CU, its fastest count there.
                     resident = self._decoder.slots(self.device, (spec.element_size, bool(spec.bit_reorder),
                                                                  bool(long_codes)))
-                    slots = max(1, min(resident, self._compute_units()))
+                    cus = self._compute_units()
+                    slots = max(1, min(resident, cus * 3 // 4 if self.prefetch else cus))
                 # a weight decoded right before its own GEMM is read back at
                 # once: ordinary stores leave it in the caches for that read
                 batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype], slots=slots,
@@ -732,14 +736,16 @@ class NeuralZipRuntime:
         """Wrap the capture of whole forwards into a HIP graph (torch.cuda.graph):
         no side-stream decode is pending from before the capture or left
         pending after it, and the last block does not prefetch the first
-        (each replay decodes it at its start)."""
+        (each replay decodes it at its start). From then on eager forwards do
+        not prefetch the first block either: a replay rewrites the slots
+        without the runtime knowing, so each forward decodes its first block
+        itself."""
         self.drain()
         self._wrap = False
         try:
             yield self
         finally:
             self.drain()
-            self._wrap = True
 
     @torch.no_grad()
     def materialized_weights(self):

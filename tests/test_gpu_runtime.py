@@ -95,10 +95,78 @@ def test_prefetch_uses_distinct_slots_and_side_stream():
         assert exact(y, expected)
 
 
+def _block_stack(n_blocks, width=512, seed=11):
+    model = nn.Module()
+    model.blocks = nn.ModuleList([nn.Sequential(nn.Linear(width, width, bias=False, dtype=torch.bfloat16),
+                                                nn.GELU()) for _ in range(n_blocks)])
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    named = {n: p.detach().clone() for n, p in model.named_parameters()}
+    return model, copy.deepcopy(model).cuda(), named
+
+
+def _run(blocks, x):
+    for block in blocks:
+        x = block(x)
+    return x
+
+
+def test_prefetch_out_of_order_and_overwritten_workspace():
+    """Outputs stay bitwise equal in order, with blocks called out of order
+    or twice in a row, and after the workspace is overwritten."""
+    model, reference, named = _block_stack(9)
+    setup = NeuralZipSetup(chunk_size=65536).build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
+    assert runtime.prefetch
+    x = torch.randn(8, 512, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).cuda()
+    expected = _run(reference.blocks, x)
+    for _ in range(3):
+        assert exact(_run(model.blocks, x), expected)
+    for order in ([5, 5, 2, 8, 0], [3, 4, 3, 1]):
+        for i in order:
+            assert exact(model.blocks[i](x), reference.blocks[i](x)), f"block {i} of {order}"
+    runtime.drain()
+    torch.cuda.synchronize()
+    for workspace in runtime.workspaces.values():
+        workspace.view(torch.uint8).fill_(0xA5)
+    assert exact(_run(model.blocks, x), expected)
+
+
+def test_graph_replays_match_eager():
+    """A forward captured in a HIP graph with graph_capture(), the side-stream
+    decodes included, gives on every replay the uncompressed model's bits,
+    with eager work on the same weights and other inputs between replays."""
+    model, reference, named = _block_stack(7, seed=12)
+    setup = NeuralZipSetup(chunk_size=65536).build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
+    g = torch.Generator().manual_seed(5)
+    inputs = [torch.randn(4, 512, generator=g).to(torch.bfloat16).cuda() for _ in range(4)]
+    static = inputs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.no_grad(), torch.cuda.stream(side):
+        _run(model.blocks, static)   # warm-up before the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), runtime.graph_capture(), torch.cuda.graph(graph):
+        out = _run(model.blocks, static)
+    with torch.no_grad():
+        for k, x in enumerate(inputs * 2):
+            static.copy_(x)
+            graph.replay()
+            got = out.clone()
+            eager = _run(model.blocks, inputs[(k + 1) % len(inputs)])   # eager work between replays
+            torch.cuda.synchronize()
+            assert exact(got, _run(reference.blocks, x)), f"replay {k}"
+            assert exact(eager, _run(reference.blocks, inputs[(k + 1) % len(inputs)])), f"eager after replay {k}"
+
+
 @pytest.mark.parametrize("decode_slots", [None, 512, 3])
 def test_block_launch_workgroups(decode_slots):
-    """Block launches use one workgroup per CU by default, or the count
-    asked for; every count decodes the same bits."""
+    """Block launches that prefetch use one workgroup on three CUs in four
+    by default, or the count asked for; every count decodes the same bits."""
     from neuralzip_amd import _native
     model = nn.Module()
     model.blocks = nn.ModuleList([nn.Sequential(nn.Linear(4096, 4096, bias=False, dtype=torch.bfloat16),
@@ -120,7 +188,8 @@ def test_block_launch_workgroups(decode_slots):
     for batches in runtime._prepared_batches.values():
         for batch in batches:
             if decode_slots is None:
-                assert 1 < batch.n_segments <= min(cus, resident)
+                assert runtime.prefetch
+                assert 1 < batch.n_segments <= min(cus * 3 // 4, resident)
             elif decode_slots == 3:   # a launch has at least one segment per codebook run
                 assert batch.n_segments <= max(3, len(runtime.export.codebooks) + 1)
             else:
