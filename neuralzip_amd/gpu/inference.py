@@ -32,6 +32,12 @@ RUNTIME_ATTRIBUTE = "neuralzip_runtime"
 # Decode units of the runtime: whole hook blocks (the reference's), or single
 # weights decoded right before their own forward.
 GRANULARITIES = ("block", "linear")
+# Inside a replayed HIP graph every ordering between the compute stream and
+# the side stream costs time of its own, tens of microseconds per block.
+# Decoding block N+1 beside block N pays for that only when a block's decode
+# is long: graph_capture() keeps the side stream for blocks of at least this
+# many decoded bytes on average and decodes smaller ones on the compute stream.
+GRAPH_PREFETCH_MIN_BYTES = 64 << 20
 _GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
 # Tensor offsets in a workspace: 128 elements keeps views 256-byte aligned
 # and fragment starts 16-element aligned (the layout's vector alignment).
@@ -498,6 +504,7 @@ class NeuralZipRuntime:
             self._events = {name: (torch.cuda.Event(), torch.cuda.Event()) for name in order} if self.prefetch else {}
         self._pending = None   # (unit name, event) decoded ahead on the side stream
         self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
+        self._side_off = False  # graph_capture() decodes on the compute stream only
         self._matvec, self._matvec_blocks, self._partials = {}, frozenset(), None
         self._fused = set()    # blocks whose current call runs the fused products
         if self.matvec_tokens:
@@ -710,7 +717,7 @@ class NeuralZipRuntime:
             if pending is not None:
                 current.wait_event(pending[1])   # the side stream must not still write a slot
             self._launch(block_name, current)
-        if self.side_stream is None:
+        if self.side_stream is None or self._side_off:
             return
         following = self._following[block_name]
         if following == block_name or (not self._wrap and following == self.units[0]):
@@ -732,20 +739,29 @@ class NeuralZipRuntime:
             self._pending = None
 
     @contextlib.contextmanager
-    def graph_capture(self):
+    def graph_capture(self, prefetch=None):
         """Wrap the capture of whole forwards into a HIP graph (torch.cuda.graph):
         no side-stream decode is pending from before the capture or left
         pending after it, and the last block does not prefetch the first
         (each replay decodes it at its start). From then on eager forwards do
         not prefetch the first block either: a replay rewrites the slots
         without the runtime knowing, so each forward decodes its first block
-        itself."""
+        itself.
+
+        `prefetch`: capture block N+1's decode on the side stream (True) or
+        every decode on the compute stream (False); None decides by the mean
+        decoded bytes per block (GRAPH_PREFETCH_MIN_BYTES)."""
+        if prefetch is None:
+            decoded = sum(g.encoded.raw_bytes for g in self.export.groups)
+            prefetch = decoded >= GRAPH_PREFETCH_MIN_BYTES * max(len(self.units), 1)
         self.drain()
         self._wrap = False
+        self._side_off = not prefetch
         try:
             yield self
         finally:
             self.drain()
+            self._side_off = False
 
     @torch.no_grad()
     def materialized_weights(self):

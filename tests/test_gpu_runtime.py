@@ -134,10 +134,12 @@ def test_prefetch_out_of_order_and_overwritten_workspace():
     assert exact(_run(model.blocks, x), expected)
 
 
-def test_graph_replays_match_eager():
-    """A forward captured in a HIP graph with graph_capture(), the side-stream
-    decodes included, gives on every replay the uncompressed model's bits,
-    with eager work on the same weights and other inputs between replays."""
+@pytest.mark.parametrize("prefetch", [None, True])
+def test_graph_replays_match_eager(prefetch):
+    """A forward captured in a HIP graph with graph_capture() (small blocks:
+    decoded on the compute stream by default; forced: side-stream decodes
+    captured too) gives on every replay the uncompressed model's bits, with
+    eager work on the same weights and other inputs between replays."""
     model, reference, named = _block_stack(7, seed=12)
     setup = NeuralZipSetup(chunk_size=65536).build(named)
     runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
@@ -150,7 +152,7 @@ def test_graph_replays_match_eager():
         _run(model.blocks, static)   # warm-up before the capture
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.no_grad(), runtime.graph_capture(), torch.cuda.graph(graph):
+    with torch.no_grad(), runtime.graph_capture(prefetch), torch.cuda.graph(graph):
         out = _run(model.blocks, static)
     with torch.no_grad():
         for k, x in enumerate(inputs * 2):
