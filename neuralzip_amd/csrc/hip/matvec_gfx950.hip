@@ -33,8 +33,14 @@
 
 namespace {
 
-constexpr int kMatvecWaves = 16;
-constexpr int kMatvecThreads = kMatvecWaves * NZ_WAVE;
+// Wavefronts per workgroup of the fused kernel, by activation rows: 16 (eight
+// per SIMD within 64 VGPRs) for one row; 12 (six per SIMD within 80 VGPRs)
+// for two to four, whose accumulators and activation vectors spill at 64.
+// Either way two workgroups share a CU's LDS.
+template <int BT>
+constexpr int matvec_waves() { return BT == 1 ? 16 : 12; }
+template <int BT>
+constexpr int matvec_threads() { return matvec_waves<BT>() * NZ_WAVE; }
 constexpr int kReduceThreads = 256;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -335,14 +341,14 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
 }
 
 template <int ES, bool REORDER, bool LONG, int BT>
-__global__ __launch_bounds__(kMatvecThreads) __attribute__((amdgpu_waves_per_eu(8)))
+__global__ __launch_bounds__(matvec_threads<BT>()) __attribute__((amdgpu_waves_per_eu(BT == 1 ? 8 : 6)))
 void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
                       const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs, nz_matvec_group group,
                       const uint8_t* __restrict__ xp, uint32_t batch, float* __restrict__ partials_p, uint32_t n_tiles) {
     const uint32_t cols = group.cols;
     using G = Geometry<ES>;
     __shared__ __align__(16) uint32_t s_lut[NZ_LUT_MAX_WORDS];
-    __shared__ __align__(16) uint8_t s_stage[kMatvecWaves][G::kStage];
+    __shared__ __align__(16) uint8_t s_stage[matvec_waves<BT>()][G::kStage];
     __shared__ uint32_t s_claim;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / NZ_WAVE);
     const uint32_t lane = threadIdx.x % NZ_WAVE;
@@ -367,7 +373,7 @@ void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
     // malformed one from overwriting the staging areas behind s_lut
     const uint32_t words = min(reinterpret_cast<const uint32_t*>(img)[2], uint32_t(NZ_LUT_MAX_WORDS));
     uint4* dst = reinterpret_cast<uint4*>(s_lut);
-    for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kMatvecThreads) dst[i] = img[i];
+    for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += matvec_threads<BT>()) dst[i] = img[i];
     __syncthreads();
     if constexpr (LONG) {
         huffman_segment<ES, REORDER, true, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave],
@@ -445,7 +451,7 @@ template <int ES, bool REORDER, bool LONG, int BT>
 hipError_t launch_matvec(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
                          const nz_matvec_group& group, const void* x, uint32_t batch, float* partials,
                          uint32_t n_tiles, hipStream_t stream) {
-    hipLaunchKernelGGL((nz_matvec_kernel<ES, REORDER, LONG, BT>), dim3(n_segs), dim3(kMatvecThreads), 0, stream,
+    hipLaunchKernelGGL((nz_matvec_kernel<ES, REORDER, LONG, BT>), dim3(n_segs), dim3(matvec_threads<BT>()), 0, stream,
                        static_cast<const uint8_t*>(base), static_cast<const nz_frag_desc*>(frags),
                        static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs), group,
                        static_cast<const uint8_t*>(x), batch, partials, n_tiles);
