@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 6
+#define NZ_ABI_VERSION 7
 
 enum nz_status {
     NZ_OK = 0,
@@ -179,6 +179,40 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
 int nz_decode_launch_ex(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
                         uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
                         uint32_t flags, void* stream);
+
+/* The arguments of one nz_decode_launch_ex call but its stream. */
+typedef struct nz_decode_args {
+    const void* base;
+    const nz_frag_desc* frags;
+    const nz_tile* tiles;
+    const nz_work* segments;
+    void* out;
+    uint32_t n_segments;
+    int32_t element_size;
+    int32_t bit_reorder;
+    int32_t long_codes;
+    uint32_t flags;
+    uint32_t reserved;   /* 0 */
+} nz_decode_args;
+
+/* A device event for ordering decodes between streams (no timing). */
+int nz_event_create(void** event);
+int nz_event_destroy(void* event);
+
+/* The stream work of one decode-hook call, in one call:
+ *   1. if `wait` is not NULL, `stream` waits for it;
+ *   2. the `n_inline` launches of `inline_launches` run on `stream`;
+ *   3. if `n_ahead` > 0: `ready` is recorded on `stream`, `side` waits for
+ *      it, the `n_ahead` launches of `ahead_launches` run on `side` (so they
+ *      start after everything queued on `stream` so far) and `done` is
+ *      recorded on `side`.
+ * Events come from nz_event_create. Replaces the stream and event calls of
+ * the reference's pre-forward hook and of this runtime's side-stream
+ * prefetch of block N+1 (neuralzip/gpu/inference.py:476-493), which cost a
+ * Python-level call each. Works under HIP stream capture: the records and
+ * waits become the graph's dependencies between the two streams. */
+int nz_decode_schedule(const nz_decode_args* inline_launches, uint32_t n_inline, const nz_decode_args* ahead_launches,
+                       uint32_t n_ahead, void* wait, void* ready, void* done, void* stream, void* side);
 
 /* CPU emulation of nz_decode_launch on host copies of the same arrays; a
  * test hook for GPU-less hosts, never used by the runtime. */

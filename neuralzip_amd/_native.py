@@ -65,7 +65,7 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 6
+ABI_VERSION = 7
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
@@ -101,6 +101,9 @@ def lib():
         L.nz_decode_slots.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
         L.nz_decode_launch_ex.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, vp]
+        L.nz_event_create.argtypes = [ctypes.POINTER(vp)]
+        L.nz_event_destroy.argtypes = [vp]
+        L.nz_decode_schedule.argtypes = [vp, u32, vp, u32, vp, vp, vp, vp, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         L.nz_matvec_plan.argtypes = [vp, vp, u32, vp, u32, u32, ctypes.c_int, vp, vp, u32, ctypes.POINTER(u32)]
         L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, u32,
@@ -257,6 +260,45 @@ def decode_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, elem
     check(lib().nz_decode_launch_ex(base_ptr, frags_ptr, tiles_ptr, segments_ptr, int(n_segments),
                                     int(element_size), int(bit_reorder), int(long_codes), out_ptr, int(flags),
                                     stream_ptr))
+
+
+class DecodeArgs(ctypes.Structure):
+    """nz_decode_args: one nz_decode_launch_ex call's arguments but the stream."""
+    _fields_ = [("base", ctypes.c_void_p), ("frags", ctypes.c_void_p), ("tiles", ctypes.c_void_p),
+                ("segments", ctypes.c_void_p), ("out", ctypes.c_void_p), ("n_segments", ctypes.c_uint32),
+                ("element_size", ctypes.c_int32), ("bit_reorder", ctypes.c_int32), ("long_codes", ctypes.c_int32),
+                ("flags", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+assert ctypes.sizeof(DecodeArgs) == 64
+
+
+def decode_args(launches):
+    """A DecodeArgs array from prepared launch arguments (base, frags, tiles,
+    segments, n_segments, element_size, bit_reorder, long_codes, out, flags)."""
+    array = (DecodeArgs * len(launches))()
+    for item, (base, frags, tiles, segs, n, es, reorder, long_codes, out, flags) in zip(array, launches):
+        item.base, item.frags, item.tiles, item.segments, item.out = base, frags, tiles, segs, out
+        item.n_segments, item.element_size, item.bit_reorder, item.long_codes = n, es, reorder, long_codes
+        item.flags = flags
+    return array
+
+
+def event_create():
+    """A device event (no timing) of the current device, as an integer handle."""
+    handle = ctypes.c_void_p()
+    check(lib().nz_event_create(ctypes.byref(handle)))
+    return handle.value
+
+
+def event_destroy(handle):
+    check(lib().nz_event_destroy(handle))
+
+
+def decode_schedule(inline, ahead, wait, ready, done, stream, side):
+    """nz_decode_schedule: `inline` and `ahead` are DecodeArgs arrays (or None)."""
+    check(lib().nz_decode_schedule(inline, len(inline) if inline is not None else 0, ahead,
+                                   len(ahead) if ahead is not None else 0, wait, ready, done, stream, side))
 
 
 def emulate_decode(base, descs, tiles, segments, element_size, bit_reorder, out):

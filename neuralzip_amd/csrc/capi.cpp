@@ -40,6 +40,10 @@ extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const v
                                     int cached, void* stream, char* message, size_t message_size);
 extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_codes, int* out, char* message,
                                    size_t message_size);
+extern "C" int nz_hip_event_create(void** event, char* message, size_t message_size);
+extern "C" int nz_hip_event_destroy(void* event, char* message, size_t message_size);
+extern "C" int nz_hip_event_record(void* event, void* stream, char* message, size_t message_size);
+extern "C" int nz_hip_stream_wait(void* stream, void* event, char* message, size_t message_size);
 extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
                                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
@@ -242,6 +246,47 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
                      void* stream) {
     return nz_decode_launch_ex(base, frags, tiles, segments, n_segments, element_size, bit_reorder, long_codes, out,
                                0, stream);
+}
+
+int nz_event_create(void** event) {
+    if (!event) return set_error(nz::kInvalidArgument, "Null event argument.");
+    char message[256] = {0};
+    const int rc = nz_hip_event_create(event, message, sizeof message);
+    return rc ? set_error(rc, message) : 0;
+}
+
+int nz_event_destroy(void* event) {
+    if (!event) return 0;
+    char message[256] = {0};
+    const int rc = nz_hip_event_destroy(event, message, sizeof message);
+    return rc ? set_error(rc, message) : 0;
+}
+
+int nz_decode_schedule(const nz_decode_args* inline_launches, uint32_t n_inline, const nz_decode_args* ahead_launches,
+                       uint32_t n_ahead, void* wait, void* ready, void* done, void* stream, void* side) {
+    if ((n_inline && !inline_launches) || (n_ahead && (!ahead_launches || !ready || !done)))
+        return set_error(nz::kInvalidArgument, "Null decode schedule argument.");
+    for (uint32_t i = 0; i < n_inline + n_ahead; ++i) {
+        const nz_decode_args& a = i < n_inline ? inline_launches[i] : ahead_launches[i - n_inline];
+        if (a.reserved != 0) return set_error(nz::kInvalidArgument, "nz_decode_args.reserved must be 0.");
+    }
+    char message[256] = {0};
+    int rc = wait ? nz_hip_stream_wait(stream, wait, message, sizeof message) : 0;
+    if (rc) return set_error(rc, message);
+    auto run = [&](const nz_decode_args& a, void* on) {
+        return nz_decode_launch_ex(a.base, a.frags, a.tiles, a.segments, a.n_segments, a.element_size, a.bit_reorder,
+                                   a.long_codes, a.out, a.flags, on);
+    };
+    for (uint32_t i = 0; i < n_inline; ++i)
+        if ((rc = run(inline_launches[i], stream)) != 0) return rc;
+    if (!n_ahead) return 0;
+    if ((rc = nz_hip_event_record(ready, stream, message, sizeof message)) != 0 ||
+        (rc = nz_hip_stream_wait(side, ready, message, sizeof message)) != 0)
+        return set_error(rc, message);
+    for (uint32_t i = 0; i < n_ahead; ++i)
+        if ((rc = run(ahead_launches[i], side)) != 0) return rc;
+    if ((rc = nz_hip_event_record(done, side, message, sizeof message)) != 0) return set_error(rc, message);
+    return 0;
 }
 
 int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,

@@ -311,3 +311,42 @@ extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_c
     return 0;
 }
 
+
+// Device events and stream ordering for nz_decode_schedule.
+extern "C" int nz_hip_event_create(void** event, char* message, size_t message_size) {
+    hipEvent_t e = nullptr;
+    const hipError_t rc = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "event creation failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    *event = e;
+    return 0;
+}
+
+extern "C" int nz_hip_event_destroy(void* event, char* message, size_t message_size) {
+    const hipError_t rc = hipEventDestroy(static_cast<hipEvent_t>(event));
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "event destruction failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    return 0;
+}
+
+extern "C" int nz_hip_event_record(void* event, void* stream, char* message, size_t message_size) {
+    const hipError_t rc = hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream));
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "event record failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    return 0;
+}
+
+extern "C" int nz_hip_stream_wait(void* stream, void* event, char* message, size_t message_size) {
+    const hipError_t rc = hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0);
+    if (rc != hipSuccess) {
+        snprintf(message, message_size, "stream wait failed: %s", hipGetErrorString(rc));
+        return -6;
+    }
+    return 0;
+}

@@ -12,6 +12,7 @@ workspace slot, ordered after everything already queued on the compute
 stream (which includes the last reads of that slot, by block N-1).
 """
 import contextlib
+import weakref
 from collections import defaultdict
 from dataclasses import dataclass, field
 from functools import cached_property, partial
@@ -394,6 +395,18 @@ def _binding_module(model, binding):
     return module
 
 
+def _current_stream_handle(device):
+    """The device's current HIP stream as an integer handle."""
+    return torch._C._cuda_getCurrentRawStream(device.index)
+
+
+def _destroy_events(device, events):
+    if events and torch.cuda.is_initialized():
+        with torch.cuda.device(device):
+            for event in events:
+                _native.event_destroy(event)
+
+
 class NeuralZipRuntime:
     """Runtime attached to one model on one device (inference.py:379-509).
 
@@ -500,8 +513,15 @@ class NeuralZipRuntime:
         for group in exported.groups:
             self._groups_by_block[group.block_name].append(group)
         self.side_stream = torch.cuda.Stream(self.device) if self.prefetch else None
+        self._side_handle = self.side_stream.cuda_stream if self.prefetch else None
+        # each unit's launches as one argument array: a hook's stream work is
+        # a single nz_decode_schedule call
+        self._schedule_args = {name: _native.decode_args([b.launch_args for b in batches])
+                               for name, batches in self._prepared_batches.items()}
         with torch.cuda.device(self.device):
-            self._events = {name: (torch.cuda.Event(), torch.cuda.Event()) for name in order} if self.prefetch else {}
+            self._events = ({name: (_native.event_create(), _native.event_create()) for name in order}
+                            if self.prefetch else {})
+        weakref.finalize(self, _destroy_events, self.device, [e for pair in self._events.values() for e in pair])
         self._pending = None   # (unit name, event) decoded ahead on the side stream
         self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
         self._side_off = False  # graph_capture() decodes on the compute stream only
@@ -700,42 +720,41 @@ class NeuralZipRuntime:
         return nn.functional.linear(input, module.weight, module.bias)
 
     def _decode_block(self, block_name, _module=None, _args=(), _kwargs=None):
-        current = torch.cuda.current_stream(self.device)
+        stream = _current_stream_handle(self.device)
         if block_name in self._matvec_blocks:
             rows = self._token_rows(_args, _kwargs)
             if rows is not None and rows <= self.matvec_tokens:
                 self._fused.add(block_name)
                 pending, self._pending = self._pending, None
                 if pending is not None:   # nothing may still write a slot once decoding resumes
-                    current.wait_event(pending[1])
+                    _native.decode_schedule(None, None, pending[1], None, None, stream, None)
                 return
             self._fused.discard(block_name)
-        pending, self._pending = self._pending, None
-        if pending is not None and pending[0] == block_name:
-            current.wait_event(pending[1])
-        else:
-            if pending is not None:
-                current.wait_event(pending[1])   # the side stream must not still write a slot
-            self._launch(block_name, current)
-        if self.side_stream is None or self._side_off:
-            return
-        following = self._following[block_name]
-        if following == block_name or (not self._wrap and following == self.units[0]):
-            return
-        # everything queued so far (the last readers of `following`'s slot
-        # included) completes before the side stream overwrites that slot;
-        # an event's later records do not change waits already queued on it
-        ready, done = self._events[following]
-        ready.record(current)
-        self.side_stream.wait_event(ready)
-        self._launch(following, self.side_stream)
-        done.record(self.side_stream)
-        self._pending = (following, done)
+        pending = self._pending
+        # wait for the side stream (for this block's prefetch, or so that it
+        # no longer writes a slot), then decode this block unless prefetched
+        wait = pending[1] if pending is not None else None
+        inline = None if pending is not None and pending[0] == block_name else self._schedule_args[block_name]
+        ahead = ready = done = following = None
+        if self.side_stream is not None and not self._side_off:
+            following = self._following[block_name]
+            if following == block_name or (not self._wrap and following == self.units[0]):
+                following = None
+            else:
+                # recorded after everything queued so far (the last readers of
+                # `following`'s slot included): the side stream overwrites the
+                # slot only then; later records of an event do not change
+                # waits already queued on it
+                ready, done = self._events[following]
+                ahead = self._schedule_args[following]
+        _native.decode_schedule(inline, ahead, wait, ready, done, stream, self._side_handle)
+        self._pending = (following, done) if following is not None else None
 
     def drain(self):
         """Order the compute stream after any pending side-stream decode."""
         if self._pending is not None:
-            torch.cuda.current_stream(self.device).wait_event(self._pending[1])
+            _native.decode_schedule(None, None, self._pending[1], None, None, _current_stream_handle(self.device),
+                                    None)
             self._pending = None
 
     @contextlib.contextmanager

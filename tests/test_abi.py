@@ -101,3 +101,25 @@ def test_no_alloc_product_refuses_more_partials_than_its_array():
                                dummy.ctypes.data, 1, None, 0, 2, 1, ctypes.addressof(weights), 1, 2048,
                                dummy.ctypes.data, 4, dummy.ctypes.data, dummy.ctypes.data, None)
     assert rc == -4 and b"no-allocation" in lib.nz_last_error()
+
+
+def test_decode_args_layout_and_schedule_checks():
+    """nz_decode_args is 64 bytes with the header's field order (the ctypes
+    mirror is checked against offsets computed from the declaration), and
+    nz_decode_schedule rejects missing arrays and events before any HIP
+    call; with nothing to do it returns 0 without touching a device."""
+    text = re.search(r"typedef struct nz_decode_args \{(.*?)\} nz_decode_args;", HEADER.read_text(), re.S).group(1)
+    names = re.findall(r"(\w+);", re.sub(r"/\*.*?\*/", "", text, flags=re.S))
+    assert names == [f[0] for f in _native.DecodeArgs._fields_]
+    sizes = [8] * 5 + [4] * 6
+    offsets = [sum(sizes[:k]) for k in range(len(sizes))]
+    assert [getattr(_native.DecodeArgs, n).offset for n in names] == offsets and ctypes.sizeof(_native.DecodeArgs) == 64
+    lib = _native.lib()
+    one = _native.decode_args([(1, 2, 3, 4, 5, 2, 1, 0, 6, 0)])
+    assert lib.nz_decode_schedule(None, 1, None, 0, None, None, None, None, None) == -1
+    assert lib.nz_decode_schedule(None, 0, one, 1, None, None, None, None, None) == -1
+    bad = _native.decode_args([(1, 2, 3, 4, 5, 2, 1, 0, 6, 0)])
+    bad[0].reserved = 1
+    assert lib.nz_decode_schedule(bad, 1, None, 0, None, None, None, None, None) == -1
+    assert b"reserved" in lib.nz_last_error()
+    assert lib.nz_decode_schedule(None, 0, None, 0, None, None, None, None, None) == 0
