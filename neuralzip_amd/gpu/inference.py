@@ -432,6 +432,8 @@ class NeuralZipRuntime:
         self.model = model
         self.export = exported
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.granularity = granularity
         # one weight at a time, decoded inline right before its own forward:
         # nothing to prefetch into
