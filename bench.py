@@ -10,14 +10,13 @@ chunk of the set from HBM-resident compressed data into an HBM workspace.
 Prints one JSON line: value = decoded GB/s (bytes written / time of `steps`
 whole steps run back to back between two HIP events on the launch stream),
 plus the roofline of the dominant decode kernel (algorithmic bytes per
-launch / its mean duration over `steps` back-to-back launches, timed the same
-way), a CPU baseline (the oracle's threaded storage decode of the same
+launch / its mean duration in those timed steps; the workload is one launch
+per step), a CPU baseline (the oracle's threaded storage decode of the same
 tensors on this host) and, under "model", the tok/s half of the metric: a
 Llama-3-8B-shaped model (random bf16 weights) generating greedily at batch 1
 uncompressed and through the NeuralZip runtime, eager and with each decode
 step replayed from a HIP graph, logits and tokens compared bit for bit. The
-model part runs first (about a minute), which also brings the device's
-clocks up before the kernel is timed.
+model part runs first (about a minute).
 """
 import argparse
 import contextlib
@@ -554,16 +553,21 @@ def main():
     torch.cuda.synchronize(device)
     total_ms = begin.elapsed_time(end)
     ms_per_step = total_ms / args.steps
-    # each launch of the step on its own, `steps` times back to back: its mean duration
-    launch_ms = []
-    for batch in batches:
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(args.steps):
-            decoder.decode_batch(batch, stream)
-        b.record(stream)
-        torch.cuda.synchronize(device)
-        launch_ms.append(a.elapsed_time(b) / args.steps)
+    # the dominant launch's mean duration: with one launch per step, the timed
+    # steps themselves; otherwise each launch on its own, `steps` times back
+    # to back right after them
+    if len(batches) == 1:
+        launch_ms = [ms_per_step]
+    else:
+        launch_ms = []
+        for batch in batches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(args.steps):
+                decoder.decode_batch(batch, stream)
+            b.record(stream)
+            torch.cuda.synchronize(device)
+            launch_ms.append(a.elapsed_time(b) / args.steps)
     dominant = max(range(len(batches)), key=lambda k: launch_ms[k])
     achieved = batches[dominant].algorithmic_bytes / (launch_ms[dominant] * 1e-3) / 1e9
     log(f"{ms_per_step:.4f} ms/step, launches {[round(m, 4) for m in launch_ms]} ms")
