@@ -267,7 +267,8 @@ def graph_generate(model, ids, new_tokens, runtime=None):
     return seconds, replays, torch.cat(generated, dim=1)
 
 
-def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=None, new_tokens=None, graph=True):
+def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=None, new_tokens=None, graph=True,
+              fused_graph=False):
     """Greedy generation on a model shape of MODELS, uncompressed and with the
     NeuralZip runtime attached, on one GPU: eager Transformers generation
     (the reference's protocol: host-bound at small batches) and, with
@@ -380,6 +381,23 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                       "tokens_identical_to_uncompressed": bool(torch.equal(nz_graph[2].cpu(), base_graph[2].cpu())),
                       "uncompressed_graph_tokens_identical_to_eager": bool(torch.equal(base_graph[2].cpu(),
                                                                     base_out[:, prompt:].cpu()))}
+    fused_info = None
+    if fused_graph and graph and not matvec:
+        # the same compressed weights with fused decode-matvec products for
+        # one-token steps: graph-replayed steps only; not bit-identical to the
+        # GEMM, so the tokens follow bf16 only for a while
+        runtime = runtime.replace(matvec_tokens=1)
+        torch.cuda.empty_cache()
+        fused = graph_generate(model, ids, new_tokens, runtime)
+        f_ms = fused[0] / fused[1] * 1e3
+        log(f"neuralzip fused graph: {f_ms:.3f} ms per replayed step")
+        fused_info = {"neuralzip_ms_per_step": round(f_ms, 3),
+                      "uncompressed_ms_per_step": round(base_graph[0] / base_graph[1] * 1e3, 3),
+                      "ratio_vs_uncompressed": round(f_ms / (base_graph[0] / base_graph[1] * 1e3), 3),
+                      "matching_token_prefix": int((fused[2].cpu() == base_graph[2].cpu()).all(0).int().cumprod(0).sum()),
+                      "bit_exact": False,
+                      "what": "fused decode-matvec products for one-token steps (matvec_tokens=1): fp32 accumulation, "
+                              "one rounding, not bit-identical to the GEMM"}
     line = {
         "metric": f"tok/s {kind} shape bs={batch} vs uncompressed {dtype_name}",
         "value": round(tok_s, 2),
@@ -408,6 +426,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "graph": graph_info,
+        "graph_fused": fused_info,
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
         "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
         # generated tokens before the first position where any sequence differs
@@ -437,6 +456,7 @@ def model_summary(line):
                       "ratio_vs_uncompressed": line["ratio_vs_uncompressed"],
                       "ms_per_step": line["ms_per_step"]},
             "graph": line["graph"],
+            "graph_fused": line["graph_fused"],
             "full_decode_pass_ms": line["config"]["full_decode_pass_ms"],
             "full_decode_pass_gbps": line["config"]["full_decode_pass_gbps"],
             "logits_bitwise_equal": line["logits_bitwise_equal"],
@@ -485,7 +505,7 @@ def main():
     model = None
     if not args.no_model:
         # the tok/s half of the metric: Llama-3-8B shape, batch 1, bit-exact decode path
-        model = model_summary(run_model("llama3-8b", graph=not args.no_graph))
+        model = model_summary(run_model("llama3-8b", graph=not args.no_graph, fused_graph=True))
         log(f"model: eager ratio {model['eager']['ratio_vs_uncompressed']}, graph ratio "
             f"{model['graph']['ratio_vs_uncompressed'] if model['graph'] else None}")
 

@@ -759,6 +759,28 @@ class NeuralZipRuntime:
                                     None)
             self._pending = None
 
+    def replace(self, **options):
+        """A runtime over the same model and export with some options changed
+        (prefetch, matvec_tokens, decode_slots, granularity); the weights stay
+        compressed. This runtime's hooks and fused forwards are removed, and
+        it must not be used afterwards."""
+        self.drain()
+        torch.cuda.current_stream(self.device).synchronize()
+        for handle in self._hook_handles:
+            handle.remove()
+        self._hook_handles.clear()
+        for module_name in self._matvec:
+            self.model.get_submodule(module_name).__dict__.pop("forward", None)
+        if getattr(self.model, RUNTIME_ATTRIBUTE, None) is self:
+            delattr(self.model, RUNTIME_ATTRIBUTE)
+        settings = dict(prefetch=self.prefetch or self.granularity != "block", matvec_tokens=self.matvec_tokens,
+                        decode_slots=self.decode_slots, granularity=self.granularity)
+        settings.update(options)
+        runtime = type(self)(self.model, self.export, self.device, **settings)
+        runtime._grad_flags = getattr(self, "_grad_flags", {})
+        runtime._install()
+        return runtime
+
     @contextlib.contextmanager
     def graph_capture(self, prefetch=None):
         """Wrap the capture of whole forwards into a HIP graph (torch.cuda.graph):

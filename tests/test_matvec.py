@@ -329,6 +329,41 @@ def test_runtime_runs_fused_products_for_few_rows_and_decodes_otherwise():
 
 
 @pytest.mark.gpu
+def test_replace_switches_a_runtime_to_fused_products_and_back():
+    """NeuralZipRuntime.replace: the same model and export with fused products
+    on, then off again; the old runtime's hooks and forwards are gone (one
+    hook per unit, one runtime attribute), and the decode path stays bitwise
+    equal to the uncompressed model."""
+    import copy
+    from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu, RUNTIME_ATTRIBUTE
+    from neuralzip_amd.setup import NeuralZipSetup
+    model = BlockStack().to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(6)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(p.dtype))
+    reference = copy.deepcopy(model).cuda()
+    named = {n: p.detach().clone() for n, p in model.named_parameters()}
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, NeuralZipSetup().build(named)), device="cuda:0")
+    x = torch.randn(1, 1, 2048, generator=g).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        want = reference(x)
+        assert torch.equal(model(x), want)
+        fused = runtime.replace(matvec_tokens=1)
+        assert getattr(model, RUNTIME_ATTRIBUTE) is fused and fused.matvec_tokens == 1
+        hooks = sum(len(m._forward_pre_hooks) for m in model.modules())
+        assert hooks == len(fused.units)
+        y = model(x)
+        # fused products round differently from the GEMM, and three bf16
+        # layers carry that on: a relative error of a few 2^-8 is the bar
+        assert fused._fused and float((y.float() - want.float()).norm() / want.float().norm()) < 0.03
+        plain = fused.replace(matvec_tokens=0)
+        assert sum(len(m._forward_pre_hooks) for m in model.modules()) == len(plain.units)
+        assert all("forward" not in m.__dict__ for m in model.modules())
+        assert torch.equal(model(x), want)
+
+
+@pytest.mark.gpu
 def test_matvec_on_a_side_stream_equals_the_current_stream():
     """HIPDecoder.matvec on a stream other than the current one, with its
     input a non-contiguous view (so the call makes its own copy), returns
