@@ -81,14 +81,25 @@ def test_clusters_separate_distinct_scales_and_setup_pickles(tmp_path):
 
 
 def test_jensen_shannon_matches_scipy():
+    """The product's distance and the oracle's restatement of it
+    (oracle/setup_ref.py) both equal scipy's base-2 Jensen-Shannon distance,
+    with zero bins in one distribution, and give 0 for identical and 1 for
+    disjoint distributions."""
     from scipy.spatial.distance import jensenshannon
     from neuralzip_amd.utils import jensen_shannon_distance
+    from oracle.setup_ref import js_distance
     rng = np.random.default_rng(4)
     for _ in range(20):
         p, q = rng.dirichlet(np.ones(256) * 0.2), rng.dirichlet(np.ones(256) * 0.2)
         p[rng.integers(0, 256, 30)] = 0
         p /= p.sum()
-        assert abs(jensen_shannon_distance(p, q) - jensenshannon(p, q, base=2)) < 1e-12
+        want = jensenshannon(p, q, base=2)
+        assert abs(jensen_shannon_distance(p, q) - want) < 1e-12
+        assert abs(js_distance(p, q) - want) < 1e-12
+    a, b = np.zeros(256), np.zeros(256)
+    a[:10], b[10:20] = 0.1, 0.1
+    for f in (jensen_shannon_distance, js_distance):
+        assert f(a, a) == 0.0 and abs(f(a, b) - 1.0) < 1e-15
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
