@@ -78,7 +78,7 @@ def _bits(t):
     return t.view(torch.int16 if t.element_size() == 2 else torch.int32)
 
 
-def run_case(kind, batches, dtype, prompt, new_tokens):
+def run_case(kind, batches, dtype, prompt, new_tokens, graph=False):
     """Uncompressed generation at each batch size, then the same with the
     runtime attached (one model, one export)."""
     from bench import MODELS, random_model
@@ -88,11 +88,15 @@ def run_case(kind, batches, dtype, prompt, new_tokens):
     model = random_model(kind, DEVICE, dtype)
     vocab = MODELS[kind][1]["vocab_size"]
     reference = {}
+    graph_tokens = None
     for batch in batches:
         ids = torch.randint(0, vocab, (batch, prompt), generator=torch.Generator().manual_seed(5 + batch)).to(DEVICE)
         with torch.no_grad():
             last = model(ids, logits_to_keep=16).logits.clone()
         reference[batch] = (ids, last, *generate(model, ids, new_tokens))
+        if graph and batch == batches[0]:
+            from bench import graph_generate
+            graph_tokens = graph_generate(model, ids, new_tokens)[2]
     sums = {name: word_checksums(p) for name, p in model.named_parameters() if p.dim() >= 2}
     log(f"{kind} {dtype}: uncompressed runs and checksums in {time.perf_counter() - t0:.0f}s")
     t0 = time.perf_counter()
@@ -121,6 +125,14 @@ def run_case(kind, batches, dtype, prompt, new_tokens):
         for step, (a, b) in enumerate(zip(logits, ref_logits)):
             assert torch.equal(_bits(a), _bits(b)), f"logits of step {step} differ at batch {batch}"
         del logits, ref_logits
+        if graph_tokens is not None and batch == batches[0]:
+            # decode steps replayed from a HIP graph captured with graph_capture()
+            from bench import graph_generate
+            got = graph_generate(model, ids, new_tokens, runtime)[2]
+            assert torch.equal(got, graph_tokens), f"graph-replayed tokens differ at batch {batch}"
+            # after replays, eager forwards still decode every block themselves
+            with torch.no_grad():
+                assert torch.equal(_bits(model(ids, logits_to_keep=16).logits), _bits(last))
     # every decoded weight, block by block, against the original's checksums
     runtime.drain()
     stream = torch.cuda.current_stream(DEVICE)
@@ -144,14 +156,16 @@ def run_case(kind, batches, dtype, prompt, new_tokens):
 
 def test_qwen2_05b_tied_embeddings():
     """Config 3: Qwen2.5-0.5B shape, tied embeddings (lm_head stays
-    resident), 128 prompt ids + 128 new tokens."""
-    run_case("qwen2-0.5b", [1], torch.bfloat16, 128, 128)
+    resident), 128 prompt ids + 128 new tokens; also greedy decode steps
+    replayed from a HIP graph (blocks decoded on the compute stream)."""
+    run_case("qwen2-0.5b", [1], torch.bfloat16, 128, 128, graph=True)
 
 
 def test_llama3_8b_batch_1_and_32():
     """Config 4: Llama-3-8B shape at batch 1 and batch 32, 512 prompt ids +
-    256 new tokens."""
-    run_case("llama3-8b", [1, 32], torch.bfloat16, 512, 256)
+    256 new tokens; also greedy decode steps at batch 1 replayed from a HIP
+    graph (block N+1 decoded on the side stream inside the graph)."""
+    run_case("llama3-8b", [1, 32], torch.bfloat16, 512, 256, graph=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
