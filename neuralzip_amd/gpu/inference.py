@@ -27,7 +27,7 @@ from neuralzip_amd._native import KIND_LONG, KIND_RAW
 from neuralzip_amd.compressor import NeuralZipCompressor
 from neuralzip_amd.dtypes import DTYPES, DTypeSpec
 from neuralzip_amd.gpu import decoder as gpu_decoder
-from neuralzip_amd.utils import _stream_chunk_size, tensor_words
+from neuralzip_amd.utils import HostStaging, _stream_chunk_size
 
 RUNTIME_ATTRIBUTE = "neuralzip_runtime"
 # Decode units of the runtime: whole hook blocks (the reference's), or single
@@ -331,12 +331,15 @@ def _assemble_export(block_order, candidates, compressor, threads=0, hooks=None)
     block_index = {name: i for i, name in enumerate(block_order)}
     offsets = defaultdict(int)
     groups, tensors = [], []
+    # device weights reach the host through one pinned buffer; the layout
+    # encoder keeps nothing of its sources, so the buffer serves every tensor
+    staging = HostStaging(max((c.parameter.numel() * c.parameter.element_size() for c in candidates), default=0))
     for member in sorted(candidates, key=lambda c: (block_index[c.block_name], c.module_name)):
         parameter = member.parameter
         config = DTYPES[parameter.dtype]
         ids = compressor.chunk_codebook_ids(member.tensor_name, parameter)
         step = _stream_chunk_size(compressor.chunk_size, config.element_size)
-        raw = tensor_words(parameter)
+        raw = staging.words(parameter)
         fragments = []
         for chunk, codebook_id in enumerate(ids.tolist()):
             if codebook_id != -1 and codebook_id not in codebooks:

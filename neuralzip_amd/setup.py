@@ -34,7 +34,7 @@ import numpy as np
 from neuralzip_amd import _native, huff0
 from neuralzip_amd.dtypes import DTYPES
 from neuralzip_amd.payloads import CHUNK_METADATA_BYTES, CodebookPayload, codebook_metadata_bytes
-from neuralzip_amd.utils import _floating_tensors, _model_tensors, _stream_chunk_size, tensor_words
+from neuralzip_amd.utils import HostStaging, _floating_tensors, _model_tensors, _stream_chunk_size
 
 _SPECS = {spec.name: spec for spec in DTYPES.values()}
 _KIND = {name: i for i, name in enumerate(_SPECS)}   # clusters never mix dtypes
@@ -92,6 +92,7 @@ class _Survey:
         self.clusters = []                # in the engine's numbering
         self.chunk_clusters = {}          # (name, dtype, lane, numel) -> cluster per chunk
         self.lane_counts = {}             # (name, dtype, lane) -> counts of the selected lane
+        self.staging = HostStaging()      # device tensors' words, one tensor at a time
 
     def _label_ids(self, name, n_chunks):
         """Native id of each chunk's forced label (-1: none): a
@@ -114,7 +115,8 @@ class _Survey:
     def add(self, name, tensor):
         spec = DTYPES[tensor.dtype]
         lane = spec.selected_stream
-        words = tensor_words(tensor)
+        # samples are copied out below, so one staging buffer serves every tensor
+        words = self.staging.words(tensor)
         step = _stream_chunk_size(self.setup.chunk_size, spec.element_size)
         histograms, lane_counts = _native.chunk_histograms(words, spec, step)
         n = len(histograms)

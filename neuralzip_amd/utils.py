@@ -66,6 +66,31 @@ def tensor_words(tensor):
     return host.reshape(-1).view(torch.uint8).numpy()
 
 
+class HostStaging:
+    """Reusable pinned host memory for the words of device tensors, one
+    tensor at a time. Copies into pinned memory run at the link's speed;
+    `.cpu()` copies into pageable memory at a fraction of it."""
+
+    def __init__(self, capacity=0):
+        self._buffer = None
+        self._capacity = int(capacity)
+
+    def words(self, tensor):
+        """The tensor's words as a flat uint8 array. For a device tensor, a
+        view of this staging memory, valid until the next call; for a CPU
+        tensor, what tensor_words returns."""
+        source = tensor.detach()
+        if source.device.type == "cpu":
+            return tensor_words(source)
+        n = source.numel() * source.element_size()
+        if self._buffer is None or self._buffer.numel() < n:
+            self._buffer = None
+            self._buffer = torch.empty(max(n, self._capacity), dtype=torch.uint8, pin_memory=True)
+        out = self._buffer[:n]
+        out.copy_(source.contiguous().reshape(-1).view(torch.uint8))
+        return out.numpy()
+
+
 def _tensor_raw_bytes(tensor):
     return tensor_words(tensor).tobytes()
 
