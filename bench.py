@@ -118,23 +118,30 @@ def copy_calibration(nbytes=1 << 30, repeats=5):
     return 0
 
 
-def copy_bandwidth(device, nbytes=1 << 30, repeats=10):
+def copy_bandwidth(device, nbytes=1 << 30, group=10, min_ms=60.0):
     """Achievable HBM bandwidth on this device: GB/s of a device-to-device
-    copy of `nbytes` (bytes read + bytes written over the mean copy time)."""
+    copy of `nbytes` (bytes read + bytes written over the copy time; the
+    median of groups of `group` back-to-back copies, timed for at least
+    `min_ms` of device time). Run right before the decode's warmup, it also
+    leaves the device in the clock state of sustained bandwidth load: after
+    an idle stretch the first ~30 decode launches otherwise run up to 15 %
+    slower than later ones."""
     src = torch.ones(nbytes, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     stream = torch.cuda.current_stream(device)
     for _ in range(3):
         dst.copy_(src)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(repeats):
-        dst.copy_(src)
-    b.record(stream)
-    torch.cuda.synchronize(device)
-    ms = a.elapsed_time(b) / repeats
+    times = []
+    while sum(times) < min_ms:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(group):
+            dst.copy_(src)
+        b.record(stream)
+        torch.cuda.synchronize(device)
+        times.append(a.elapsed_time(b))
+    ms = float(np.median(times)) / group
     del src, dst
-    torch.cuda.empty_cache()
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
