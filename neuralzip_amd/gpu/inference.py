@@ -427,7 +427,7 @@ class NeuralZipRuntime:
     """
 
     def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0, decode_slots=None,
-                 granularity="block"):
+                 granularity="block", _store=None):
         if granularity not in GRANULARITIES:
             raise ValueError(f"granularity must be one of {GRANULARITIES}.")
         if granularity == "linear" and matvec_tokens:
@@ -487,7 +487,12 @@ class NeuralZipRuntime:
             self._binding_offset[binding] = base
             self._unit_bindings[unit].append((config.torch_dtype, binding))
             frag_base += layout.n_fragments
-        self.store = gpu_decoder.DeviceStore(exported.codebooks, tensors, self.device)
+        # a store packed for the same tensors at the same offsets is taken over as is
+        self._store_key = tuple((id(layout), base) for layout, _, base in tensors)
+        if _store is not None and _store[0] == self._store_key:
+            self.store = _store[1]
+        else:
+            self.store = gpu_decoder.DeviceStore(exported.codebooks, tensors, self.device)
         self._prepared_batches = defaultdict(list)
         self.algorithmic_bytes = {}
         for (name, dtype), frags in by_unit.items():
@@ -779,7 +784,16 @@ class NeuralZipRuntime:
         settings = dict(prefetch=self.prefetch or self.granularity != "block", matvec_tokens=self.matvec_tokens,
                         decode_slots=self.decode_slots, granularity=self.granularity)
         settings.update(options)
-        runtime = type(self)(self.model, self.export, self.device, **settings)
+        # The compressed store depends only on the decode units and their
+        # slots. The new runtime takes it over when those stay; otherwise this
+        # runtime's device buffers go first, so that two copies of the
+        # compressed weights never coexist.
+        same = (settings["granularity"] == self.granularity
+                and (bool(settings["prefetch"]) and settings["granularity"] == "block") == self.prefetch)
+        store = (self._store_key, self.store) if same else None
+        self.store, self._prepared_batches, self._schedule_args = None, defaultdict(list), {}
+        self._matvec, self._group_plans, self._outputs, self._partials = {}, {}, {}, None
+        runtime = type(self)(self.model, self.export, self.device, _store=store, **settings)
         runtime._grad_flags = getattr(self, "_grad_flags", {})
         runtime._install()
         return runtime

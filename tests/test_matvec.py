@@ -331,9 +331,10 @@ def test_runtime_runs_fused_products_for_few_rows_and_decodes_otherwise():
 @pytest.mark.gpu
 def test_replace_switches_a_runtime_to_fused_products_and_back():
     """NeuralZipRuntime.replace: the same model and export with fused products
-    on, then off again; the old runtime's hooks and forwards are gone (one
-    hook per unit, one runtime attribute), and the decode path stays bitwise
-    equal to the uncompressed model."""
+    on, then off again, then per-Linear decode units; the old runtime's hooks
+    and forwards are gone (one hook per unit, one runtime attribute), the
+    compressed store is shared while the decode units stay, and the decode
+    path stays bitwise equal to the uncompressed model."""
     import copy
     from neuralzip_amd.gpu.inference import NeuralZipRuntime, export_model_for_gpu, RUNTIME_ATTRIBUTE
     from neuralzip_amd.setup import NeuralZipSetup
@@ -349,8 +350,11 @@ def test_replace_switches_a_runtime_to_fused_products_and_back():
     with torch.no_grad():
         want = reference(x)
         assert torch.equal(model(x), want)
+        store = runtime.store
         fused = runtime.replace(matvec_tokens=1)
         assert getattr(model, RUNTIME_ATTRIBUTE) is fused and fused.matvec_tokens == 1
+        # same decode units and slots: the compressed store is taken over, not rebuilt
+        assert fused.store is store and runtime.store is None
         hooks = sum(len(m._forward_pre_hooks) for m in model.modules())
         assert hooks == len(fused.units)
         y = model(x)
@@ -360,6 +364,10 @@ def test_replace_switches_a_runtime_to_fused_products_and_back():
         plain = fused.replace(matvec_tokens=0)
         assert sum(len(m._forward_pre_hooks) for m in model.modules()) == len(plain.units)
         assert all("forward" not in m.__dict__ for m in model.modules())
+        assert torch.equal(model(x), want)
+        # other decode units: a new store, built after the old one was released
+        linear = plain.replace(granularity="linear")
+        assert linear.store is not store and plain.store is None
         assert torch.equal(model(x), want)
 
 
