@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 7
+#define NZ_ABI_VERSION 8
 
 enum nz_status {
     NZ_OK = 0,
@@ -43,6 +43,7 @@ typedef struct nz_layout nz_layout;
 typedef struct nz_frag_desc nz_frag_desc;   /* 64 bytes */
 typedef struct nz_tile nz_tile;             /* 16 bytes */
 typedef struct nz_work nz_work;             /* 16 bytes */
+typedef struct nz_matvec_tile nz_matvec_tile; /* 40 bytes */
 
 const char* nz_last_error(void);
 int nz_abi_version(void);
@@ -253,18 +254,31 @@ int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_t
                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
                    uint32_t* row_index, uint32_t* entries, uint32_t capacity, uint32_t* n_entries);
 
+/* The fused kernel's per-tile records of the same product (tiles and
+ * weights as for nz_matvec_plan): out[t] holds tile t's byte offsets in the
+ * packed buffer and the stacked output row and column of its first vector
+ * (n_tiles records of 40 bytes, caller-allocated). Fails if a tile names a
+ * fragment at or past n_frags, lies outside the weights, or would read
+ * outside the packed buffer's store_bytes, so the kernel forms no address
+ * the host has not checked. No counterpart in the reference (see
+ * nz_matvec_plan). */
+int nz_matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* tiles, uint32_t n_tiles,
+                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
+                    uint64_t store_bytes, nz_matvec_tile* out);
+
 /* Fused decode and product, first pass: for every tile t of the segments
  * (a plan of nz_plan_work over the same tiles), the products of its
  * elements with x (device, batch x cols in the weights' dtype, 1 <= batch
  * <= NZ_MATVEC_MAX_BATCH) summed per row they touch, in
  * partials[(2 * t + slot) * batch + b] (device fp32, 2 * n_tiles * batch
- * values). One call per codebook kind (long_codes) of the tiles.
+ * values). `tiles` is a device copy of nz_matvec_tiles' records for `base`
+ * (the packed buffer they were checked against); `frags` gives each
+ * segment's LUT. One call per codebook kind (long_codes) of the tiles.
  * Asynchronous on `stream`. No counterpart in the reference (see
  * nz_matvec_plan). */
-int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
-                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes,
-                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
-                     uint32_t batch, float* partials, uint32_t n_tiles, void* stream);
+int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_matvec_tile* tiles,
+                     const nz_work* segments, uint32_t n_segments, int element_size, int bit_reorder, int long_codes,
+                     uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream);
 
 /* Second pass: for each weight k and row n, weights[k].y[b * rows + n] =
  * (sum of the stacked row's partials, in entry order) + bias[n], rounded
@@ -290,7 +304,7 @@ int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const n
  * clearing. No counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc). Asynchronous on `stream`. */
-int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_matvec_tile* tiles, uint32_t n_tiles,
                       const nz_work* short_segments, uint32_t n_short, const nz_work* long_segments,
                       uint32_t n_long, int element_size, int bit_reorder, const nz_matvec_weight* weights,
                       uint32_t n_weights, uint32_t cols, const void* x, uint32_t batch, const uint32_t* row_index,

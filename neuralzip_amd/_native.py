@@ -27,7 +27,12 @@ def tile_skip(tiles):
 
 
 WORK = np.dtype([("tile0", "<u4"), ("tile1", "<u4"), ("lut_frag", "<u4"), ("kind", "<u4")])
-assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16
+# nz_matvec_tile: a fused product's tile with its offsets and stacked row and
+# column resolved (head = elements of the first vector before the tile |
+# lane stride << 4)
+MATVEC_TILE = np.dtype([("bits", "<u8"), ("meta", "<u8"), ("lanes", "<u8"), ("counts", "<u4"), ("head", "<u4"),
+                        ("row0", "<u4"), ("col0", "<u4")])
+assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16 and MATVEC_TILE.itemsize == 40
 
 KIND_RAW, KIND_SHORT, KIND_LONG = 0, 1, 2
 # Words of the kernels' LDS copy of a LUT image (NZ_LUT_MAX_WORDS of nz_format.h).
@@ -65,7 +70,7 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 7
+ABI_VERSION = 8
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
@@ -106,8 +111,9 @@ def lib():
         L.nz_decode_schedule.argtypes = [vp, u32, vp, u32, vp, vp, vp, vp, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         L.nz_matvec_plan.argtypes = [vp, vp, u32, vp, u32, u32, ctypes.c_int, vp, vp, u32, ctypes.POINTER(u32)]
-        L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, u32,
-                                       vp, u32, vp, u32, vp]
+        L.nz_matvec_tiles.argtypes = [vp, u32, vp, u32, vp, u32, u32, ctypes.c_int, u64, vp]
+        L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, u32, vp, u32,
+                                       vp, u32, vp]
         L.nz_matvec_reduce.argtypes = [vp, vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         L.nz_matvec_noalloc.argtypes = [vp, vp, vp, u32, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp, u32, u32,
                                         vp, u32, vp, vp, vp]
@@ -337,12 +343,24 @@ def matvec_plan(descs, tiles, weights, cols, element_size):
     return row_index, entries[:n.value].copy()
 
 
+def matvec_tiles(descs, tiles, weights, cols, element_size, store_bytes):
+    """The fused kernel's records (MATVEC_TILE, one per tile, in the tiles'
+    order) of a product over `weights` ((workspace offset, rows) in
+    increasing order), checked against a packed buffer of store_bytes."""
+    array = matvec_weights(weights)
+    out = np.zeros(len(tiles), dtype=MATVEC_TILE)
+    check(lib().nz_matvec_tiles(descs.ctypes.data, len(descs), tiles.ctypes.data if len(tiles) else None, len(tiles),
+                                ctypes.cast(array, ctypes.c_void_p), len(weights), int(cols), int(element_size),
+                                int(store_bytes), out.ctypes.data if len(out) else None))
+    return out
+
+
 def matvec_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, element_size, bit_reorder, long_codes,
-                  weights, cols, x_ptr, batch, partials_ptr, n_tiles, stream_ptr):
-    """`weights`: a MatvecWeight array (matvec_weights)."""
+                  cols, x_ptr, batch, partials_ptr, n_tiles, stream_ptr):
+    """`tiles_ptr`: a device copy of matvec_tiles' records for this base."""
     check(lib().nz_matvec_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, int(n_segments), int(element_size),
-                                 int(bit_reorder), int(long_codes), ctypes.cast(weights, ctypes.c_void_p),
-                                 len(weights), int(cols), x_ptr, int(batch), partials_ptr, int(n_tiles), stream_ptr))
+                                 int(bit_reorder), int(long_codes), int(cols), x_ptr, int(batch), partials_ptr,
+                                 int(n_tiles), stream_ptr))
 
 
 def matvec_reduce(row_index_ptr, entries_ptr, weights, partials_ptr, batch, element_size, bit_reorder, stream_ptr):

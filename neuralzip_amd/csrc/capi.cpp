@@ -45,10 +45,9 @@ extern "C" int nz_hip_event_destroy(void* event, char* message, size_t message_s
 extern "C" int nz_hip_event_record(void* event, void* stream, char* message, size_t message_size);
 extern "C" int nz_hip_stream_wait(void* stream, void* event, char* message, size_t message_size);
 extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
-                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
-                                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
-                                    uint32_t batch, float* partials, uint32_t n_tiles, void* stream, char* message,
-                                    size_t message_size);
+                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes, uint32_t cols,
+                                    const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream,
+                                    char* message, size_t message_size);
 extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const void* tiles, uint32_t n_tiles,
                                      const void* short_segs, uint32_t n_short, const void* long_segs,
                                      uint32_t n_long, int element_size, int bit_reorder,
@@ -306,23 +305,35 @@ int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_t
     });
 }
 
-int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
-                     uint32_t n_segments, int element_size, int bit_reorder, int long_codes,
-                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
-                     uint32_t batch, float* partials, uint32_t n_tiles, void* stream) {
-    if (n_segments && (!base || !frags || !tiles || !segments || !x || !partials || !weights))
+int nz_matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* tiles, uint32_t n_tiles,
+                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
+                    uint64_t store_bytes, nz_matvec_tile* out) {
+    return guarded([&] {
+        if (!frags || (!tiles && n_tiles) || !weights || (!out && n_tiles))
+            nz::fail(nz::kInvalidArgument, "Null matvec tiles argument.");
+        if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
+        nz::matvec_tiles(frags, n_frags, tiles, n_tiles, weights, n_weights, cols,
+                         static_cast<unsigned>(element_size), store_bytes, out);
+    });
+}
+
+int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_matvec_tile* tiles,
+                     const nz_work* segments, uint32_t n_segments, int element_size, int bit_reorder, int long_codes,
+                     uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream) {
+    if (n_segments && (!base || !frags || !tiles || !segments || !x || !partials))
         return set_error(nz::kInvalidArgument, "Null matvec argument.");
     const int rc0 = guarded([&] {
         if (element_size != 2 && element_size != 4) nz::fail(nz::kInvalidArgument, "element_size must be 2 or 4.");
-        nz::check_matvec_group(weights, n_weights, cols, static_cast<unsigned>(element_size));
+        if (!cols || cols % (16u / static_cast<unsigned>(element_size)))
+            nz::fail(nz::kInvalidArgument, "Row length must be a positive multiple of 16 bytes of elements.");
         if (static_cast<uint64_t>(batch) * cols * static_cast<uint64_t>(element_size) > 0xFFFFFFFFull)
             nz::fail(nz::kInvalidArgument, "Activation rows exceed the addressable range.");
     });
     if (rc0) return rc0;
     char message[256] = {0};
     const int rc = nz_hip_matvec_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
-                                        long_codes, weights, n_weights, cols, x, batch, partials, n_tiles, stream,
-                                        message, sizeof message);
+                                        long_codes, cols, x, batch, partials, n_tiles, stream, message,
+                                        sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }
@@ -343,7 +354,7 @@ int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const n
     return 0;
 }
 
-int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
+int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_matvec_tile* tiles, uint32_t n_tiles,
                       const nz_work* short_segments, uint32_t n_short, const nz_work* long_segments,
                       uint32_t n_long, int element_size, int bit_reorder, const nz_matvec_weight* weights,
                       uint32_t n_weights, uint32_t cols, const void* x, uint32_t batch, const uint32_t* row_index,

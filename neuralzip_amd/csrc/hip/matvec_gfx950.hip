@@ -3,8 +3,9 @@
 // y[b, n] = sum_k W[n, k] * x[b, k] + bias[n] for up to four row-major
 // weights W (rows x cols each) that share the activations x, stored in the
 // layout of nz_format.h, without writing W anywhere. The weights' rows are
-// stacked in workspace order; a tile finds its weight from its first
-// element. No counterpart in the reference, which always decodes a block
+// stacked in workspace order; each tile's record (nz_matvec_tile, resolved
+// on the host) gives its addresses and its stacked row and column. No
+// counterpart in the reference, which always decodes a block
 // into its workspace before the module's own GEMM reads it
 // (neuralzip/gpu/inference.py:379-509).
 //
@@ -98,16 +99,7 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// The weights of one launch, sorted by workspace offset and disjoint; their
-// output rows are stacked in this order (weight k's first row is row_base[k]).
-struct nz_matvec_group {
-    uint64_t offset[NZ_MATVEC_MAX_WEIGHTS];   // workspace element of W[0, 0]
-    uint32_t row_base[NZ_MATVEC_MAX_WEIGHTS];
-    uint32_t count;
-    uint32_t cols;
-};
-
-// Where a tile sits in the weight: staging index i holds element
+// Where a tile sits in the product: staging index i holds element
 // (row0 + (i >= split), col0 + i - (i >= split ? cols : 0)).
 struct RowSpan {
     uint32_t row0;
@@ -115,26 +107,30 @@ struct RowSpan {
     uint32_t split;   // staging index of the next row's first element
 };
 
-// Stacked row and column of a tile's staging index 0 (`first`, a workspace
-// element): the weight is the last one of the group starting at or before it.
-// Constant indices only: the group's fields stay in scalar registers and the
-// weight is picked with selects, not with loads at a computed index.
-__device__ __forceinline__ RowSpan row_span(uint64_t first, const nz_matvec_group& g) {
-    uint64_t offset = g.offset[0];
-    uint32_t row_base = g.row_base[0];
-#pragma unroll
-    for (uint32_t k = 1; k < NZ_MATVEC_MAX_WEIGHTS; ++k) {
-        const bool later = k < g.count && first >= g.offset[k];
-        offset = later ? g.offset[k] : offset;
-        row_base = later ? g.row_base[k] : row_base;
-    }
-    const uint32_t cols = g.cols;
-    const uint32_t rel = static_cast<uint32_t>(first - offset) + row_base * cols;
-    RowSpan s;
-    s.row0 = rel / cols;
-    s.col0 = rel - s.row0 * cols;
-    s.split = cols - s.col0;
-    return s;
+// Tile t's record (nz_matvec_tile, resolved and bounds-checked on the host):
+// its addresses in the packed buffer and its place in the stacked rows. One
+// 40-byte scalar load per tile; no fragment descriptor, weight lookup or
+// division on the device.
+template <int ES>
+__device__ __forceinline__ TileInfo tile_record(const uint8_t* base, const nz_matvec_tile* tiles, uint32_t t,
+                                                uint32_t cols, RowSpan& rs) {
+    constexpr uint32_t V = Geometry<ES>::V;
+    const nz_matvec_tile r = tiles[t];
+    TileInfo ti;
+    ti.bits = base + r.bits;
+    ti.meta = reinterpret_cast<const uint16_t*>(base + r.meta);
+    ti.lanes = base + r.lanes;
+    ti.first = 0;   // only the decode kernel's addressing uses it
+    ti.stride = r.head >> 4;
+    ti.n_win = nz_tile_windows(r.counts);
+    ti.skip = nz_tile_skip(r.counts);
+    ti.s0 = r.head & 15u;
+    ti.s1 = ti.s0 + nz_tile_elements(r.counts);
+    ti.nv = (ti.s1 + V - 1) / V;
+    rs.row0 = r.row0;
+    rs.col0 = r.col0;
+    rs.split = cols - r.col0;
+    return ti;
 }
 
 // The per-tile accumulators: acc[slot][b], slot 0 = row0, slot 1 = row0 + 1.
@@ -231,11 +227,9 @@ __device__ __forceinline__ void multiply_tile(const TileInfo& ti, const Fetch<ES
 }
 
 template <int ES, bool REORDER, bool LONG, bool ESC, int BT>
-__device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,
-                                                const nz_work& seg, uint32_t* counter, uint32_t lane,
-                                                const uint32_t* lut, uint8_t* stage, const nz_matvec_group& group,
-                                                rsrc_t x, uint32_t batch, rsrc_t partials) {
-    const uint32_t cols = group.cols;
+__device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_matvec_tile* tiles, const nz_work& seg,
+                                                uint32_t* counter, uint32_t lane, const uint32_t* lut, uint8_t* stage,
+                                                uint32_t cols, rsrc_t x, uint32_t batch, rsrc_t partials) {
     const uint32_t n = seg.tile1 - seg.tile0;
     uint32_t t = claim(counter, lane);
     if (t >= n) return;
@@ -243,19 +237,20 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_fr
     // lanes and its first activations at its start, so that the decode hides
     // their latency (holding the next tile's raw lanes as well would not fit
     // the 64 registers of eight wavefronts per SIMD).
-    TileInfo cur = tile_info<ES>(base, frags, tiles, seg.tile0 + t);
+    RowSpan rs;
+    TileInfo cur = tile_record<ES>(base, tiles, seg.tile0 + t, cols, rs);
     Fetch<ES, LONG> fc;
     fetch_bits<ES, LONG>(cur, lane, fc);
     uint32_t tn = claim(counter, lane);
     Partial<BT> p;
     for (;;) {
         const bool more = tn < n;
-        const TileInfo nxt = tile_info<ES>(base, frags, tiles, seg.tile0 + (more ? tn : t));
+        RowSpan rn;
+        const TileInfo nxt = tile_record<ES>(base, tiles, seg.tile0 + (more ? tn : t), cols, rn);
         Fetch<ES, LONG> fn;
         fetch_bits<ES, LONG>(nxt, lane, fn);
         const uint32_t after = more ? claim(counter, lane) : n;
         fetch_raw<ES, LONG>(cur, lane, fc);
-        const RowSpan rs = row_span(cur.first, group);
         uint4 early[2];   // activation row 0 of rounds 0 and 1
 #pragma unroll
         for (uint32_t r = 0; r < 2; ++r) {
@@ -272,26 +267,23 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_fr
         t = tn;
         tn = after;
         cur = nxt;
+        rs = rn;
         fc = fn;
     }
 }
 
 // A raw (uncoded) tile: the exponent lane is stored as is.
 template <int ES, bool REORDER, int BT>
-__device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f, const nz_tile& tile,
-                         const nz_matvec_group& group, rsrc_t x, uint32_t batch, uint32_t lane, Partial<BT>& p) {
-    const uint32_t cols = group.cols;
+__device__ void raw_tile(const uint8_t* __restrict__ base, const nz_matvec_tile* tiles, uint32_t t, uint32_t cols,
+                         rsrc_t x, uint32_t batch, uint32_t lane, Partial<BT>& p) {
     constexpr uint32_t V = 16 / ES;
-    const uint64_t A0 = f.out + tile.out0, A1 = A0 + nz_tile_elements(tile.counts);
-    const uint64_t first = A0 / V * V;
-    const uint32_t s0 = static_cast<uint32_t>(A0 - first), s1 = static_cast<uint32_t>(A1 - first);
-    const uint32_t nv = (s1 + V - 1) / V;
-    const uint64_t origin = f.out / V * V;
-    const RowSpan rs = row_span(first, group);
+    RowSpan rs;
+    const TileInfo ti = tile_record<ES>(base, tiles, t, cols, rs);
+    const uint32_t s0 = ti.s0, s1 = ti.s1, nv = ti.nv, stride = ti.stride;
     for (uint32_t i = lane; i < nv; i += NZ_WAVE) {
         const uint32_t g = i * V;
-        const uint8_t* expo = base + f.bits + (first + g - origin);
-        const uint8_t* lanes = base + f.lanes + (first + g - origin);
+        const uint8_t* expo = ti.bits + g;     // a raw fragment's exponent lane
+        const uint8_t* lanes = ti.lanes + g;
         if (g >= s0 && g + V <= s1) {
             uint32_t e0, e1 = 0, r[3];
             if (ES == 2) {
@@ -304,8 +296,8 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
             } else {
                 e0 = *reinterpret_cast<const uint32_t*>(expo);
                 r[0] = *reinterpret_cast<const uint32_t*>(lanes);
-                r[1] = *reinterpret_cast<const uint32_t*>(lanes + f.lane_stride);
-                r[2] = *reinterpret_cast<const uint32_t*>(lanes + 2 * f.lane_stride);
+                r[1] = *reinterpret_cast<const uint32_t*>(lanes + stride);
+                r[2] = *reinterpret_cast<const uint32_t*>(lanes + 2 * stride);
             }
             const uint4 w = merge_vector<ES, REORDER>(e0, e1, r);
             const bool h = g >= rs.split;
@@ -321,7 +313,7 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
             for (uint32_t j = 0; j < V; ++j) {
                 if (g + j < s0 || g + j >= s1) continue;
                 uint32_t raw = 0;
-                for (int k = 0; k + 1 < ES; ++k) raw |= static_cast<uint32_t>(lanes[j + k * f.lane_stride]) << (8 * k);
+                for (int k = 0; k + 1 < ES; ++k) raw |= static_cast<uint32_t>(lanes[j + k * stride]) << (8 * k);
                 const float wf =
                     word_to_float<ES, REORDER>(restore_word<ES, REORDER>((static_cast<uint32_t>(expo[j]) << (8 * (ES - 1))) | raw));
                 const bool h = g + j >= rs.split;
@@ -343,9 +335,8 @@ __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_frag_desc& f
 template <int ES, bool REORDER, bool LONG, int BT>
 __global__ __launch_bounds__(matvec_threads<BT>()) __attribute__((amdgpu_waves_per_eu(BT == 1 ? 8 : 6)))
 void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
-                      const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs, nz_matvec_group group,
+                      const nz_matvec_tile* __restrict__ tiles, const nz_work* __restrict__ segs, uint32_t cols,
                       const uint8_t* __restrict__ xp, uint32_t batch, float* __restrict__ partials_p, uint32_t n_tiles) {
-    const uint32_t cols = group.cols;
     using G = Geometry<ES>;
     __shared__ __align__(16) uint32_t s_lut[NZ_LUT_MAX_WORDS];
     __shared__ __align__(16) uint8_t s_stage[matvec_waves<BT>()][G::kStage];
@@ -361,9 +352,8 @@ void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
         const uint32_t n = seg.tile1 - seg.tile0;
         Partial<BT> p;
         for (uint32_t t = claim(&s_claim, lane); t < n; t = claim(&s_claim, lane)) {
-            const nz_tile tile = tiles[seg.tile0 + t];
             p.clear();
-            raw_tile<ES, REORDER, BT>(base, frags[tile.frag], tile, group, x, batch, lane, p);
+            raw_tile<ES, REORDER, BT>(base, tiles, seg.tile0 + t, cols, x, batch, lane, p);
             p.flush(partials, seg.tile0 + t, batch, lane);
         }
         return;
@@ -376,15 +366,15 @@ void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
     for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += matvec_threads<BT>()) dst[i] = img[i];
     __syncthreads();
     if constexpr (LONG) {
-        huffman_segment<ES, REORDER, true, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut, s_stage[wave],
-                                                     group, x, batch, partials);
+        huffman_segment<ES, REORDER, true, true, BT>(base, tiles, seg, &s_claim, lane, s_lut, s_stage[wave], cols,
+                                                     x, batch, partials);
     } else {
         if (s_lut[0])
-            huffman_segment<ES, REORDER, false, true, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut,
-                                                          s_stage[wave], group, x, batch, partials);
+            huffman_segment<ES, REORDER, false, true, BT>(base, tiles, seg, &s_claim, lane, s_lut,
+                                                          s_stage[wave], cols, x, batch, partials);
         else
-            huffman_segment<ES, REORDER, false, false, BT>(base, frags, tiles, seg, &s_claim, lane, s_lut,
-                                                           s_stage[wave], group, x, batch, partials);
+            huffman_segment<ES, REORDER, false, false, BT>(base, tiles, seg, &s_claim, lane, s_lut,
+                                                           s_stage[wave], cols, x, batch, partials);
     }
 }
 
@@ -449,20 +439,20 @@ void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint3
 
 template <int ES, bool REORDER, bool LONG, int BT>
 hipError_t launch_matvec(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
-                         const nz_matvec_group& group, const void* x, uint32_t batch, float* partials,
-                         uint32_t n_tiles, hipStream_t stream) {
+                         uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles,
+                         hipStream_t stream) {
     hipLaunchKernelGGL((nz_matvec_kernel<ES, REORDER, LONG, BT>), dim3(n_segs), dim3(matvec_threads<BT>()), 0, stream,
                        static_cast<const uint8_t*>(base), static_cast<const nz_frag_desc*>(frags),
-                       static_cast<const nz_tile*>(tiles), static_cast<const nz_work*>(segs), group,
+                       static_cast<const nz_matvec_tile*>(tiles), static_cast<const nz_work*>(segs), cols,
                        static_cast<const uint8_t*>(x), batch, partials, n_tiles);
     return hipGetLastError();
 }
 
 template <int ES, bool REORDER, bool LONG>
 hipError_t launch_batch(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
-                        const nz_matvec_group& group, const void* x, uint32_t batch, float* partials,
-                        uint32_t n_tiles, hipStream_t stream) {
-#define NZ_MATVEC(BT) launch_matvec<ES, REORDER, LONG, BT>(base, frags, tiles, segs, n_segs, group, x, batch, partials, n_tiles, stream)
+                        uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles,
+                        hipStream_t stream) {
+#define NZ_MATVEC(BT) launch_matvec<ES, REORDER, LONG, BT>(base, frags, tiles, segs, n_segs, cols, x, batch, partials, n_tiles, stream)
     if (batch <= 1) return NZ_MATVEC(1);
     if (batch <= 2) return NZ_MATVEC(2);
     return NZ_MATVEC(4);
@@ -478,27 +468,14 @@ bool layout_ok(int element_size, int bit_reorder, char* message, size_t message_
 
 }  // namespace
 
-// Partial sums of one launch (one codebook kind) of a group's tiles: writes
-// partials[(2 * t + slot) * batch + b] for every tile t the segments cover.
-// The caller has validated the group (sorted, disjoint weights).
+// Partial sums of one launch (one codebook kind) of a product's tiles:
+// writes partials[(2 * t + slot) * batch + b] for every tile t the segments
+// cover. `tiles` are nz_matvec_tile records the host checked against `base`.
 extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const void* tiles, const void* segs,
-                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes,
-                                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, const void* x,
-                                    uint32_t batch, float* partials, uint32_t n_tiles, void* stream, char* message,
-                                    size_t message_size) {
+                                    uint32_t n_segs, int element_size, int bit_reorder, int long_codes, uint32_t cols,
+                                    const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream,
+                                    char* message, size_t message_size) {
     if (n_segs == 0) return 0;
-    if (n_weights == 0 || n_weights > NZ_MATVEC_MAX_WEIGHTS) {
-        snprintf(message, message_size, "matvec groups hold 1 to %d weights (got %u).", NZ_MATVEC_MAX_WEIGHTS,
-                 n_weights);
-        return -1;
-    }
-    nz_matvec_group group = {};
-    group.count = n_weights;
-    group.cols = cols;
-    for (uint32_t k = 0, base_row = 0; k < n_weights; base_row += weights[k].rows, ++k) {
-        group.offset[k] = weights[k].offset;
-        group.row_base[k] = base_row;
-    }
     if (!layout_ok(element_size, bit_reorder, message, message_size)) return -1;
     if (batch == 0 || batch > NZ_MATVEC_MAX_BATCH) {
         snprintf(message, message_size, "matvec batch must be in [1, %d] (got %u).", NZ_MATVEC_MAX_BATCH, batch);
@@ -506,7 +483,7 @@ extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const v
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t rc;
-#define NZ_BATCH(E, R, L) launch_batch<E, R, L>(base, frags, tiles, segs, n_segs, group, x, batch, partials, n_tiles, st)
+#define NZ_BATCH(E, R, L) launch_batch<E, R, L>(base, frags, tiles, segs, n_segs, cols, x, batch, partials, n_tiles, st)
     if (element_size == 2 && bit_reorder)
         rc = long_codes ? NZ_BATCH(2, true, true) : NZ_BATCH(2, true, false);
     else if (element_size == 2)
@@ -617,11 +594,11 @@ extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const 
     }
     int rc = 0;
     if (n_short)
-        rc = nz_hip_matvec_launch(base, frags, tiles, short_segs, n_short, element_size, bit_reorder, 0, weights,
-                                  n_weights, cols, x, batch, partials, n_tiles, stream, message, message_size);
+        rc = nz_hip_matvec_launch(base, frags, tiles, short_segs, n_short, element_size, bit_reorder, 0, cols, x,
+                                  batch, partials, n_tiles, stream, message, message_size);
     if (rc == 0 && n_long)
-        rc = nz_hip_matvec_launch(base, frags, tiles, long_segs, n_long, element_size, bit_reorder, 1, weights,
-                                  n_weights, cols, x, batch, partials, n_tiles, stream, message, message_size);
+        rc = nz_hip_matvec_launch(base, frags, tiles, long_segs, n_long, element_size, bit_reorder, 1, cols, x,
+                                  batch, partials, n_tiles, stream, message, message_size);
     if (rc == 0)
         rc = nz_hip_matvec_reduce(row_index, entries, weights, n_weights, partials, batch, element_size, bit_reorder,
                                   stream, message, message_size);

@@ -333,6 +333,49 @@ void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
     while (row < rows) row_index[++row] = static_cast<uint32_t>(entries.size());
 }
 
+void matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* tiles, uint32_t n_tiles,
+                  const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, unsigned element_size,
+                  uint64_t store_bytes, nz_matvec_tile* out) {
+    check_matvec_group(weights, n_weights, cols, element_size);
+    const uint64_t V = 16 / element_size;
+    std::vector<uint64_t> row_base(n_weights);
+    for (uint32_t k = 0, rows = 0; k < n_weights; rows += weights[k].rows, ++k) row_base[k] = rows;
+    // [offset, offset + bytes) inside the packed buffer
+    auto inside = [&](uint64_t offset, uint64_t bytes) { return offset <= store_bytes && bytes <= store_bytes - offset; };
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const nz_tile& tile = tiles[t];
+        if (tile.frag >= n_frags) fail(kInvalidArgument, "A tile names a fragment past the descriptors.");
+        const nz_frag_desc& f = frags[tile.frag];
+        const uint64_t a0 = f.out + tile.out0;
+        const uint64_t first = a0 / V * V, origin = f.out / V * V;
+        const uint32_t elements = nz_tile_elements(tile.counts), windows = nz_tile_windows(tile.counts);
+        // weight offsets are multiples of V, so `first` and a0 fall in the same weight
+        uint32_t w = 0;
+        for (uint32_t k = 1; k < n_weights; ++k)
+            if (first >= weights[k].offset) w = k;
+        const uint64_t lo = weights[w].offset, hi = lo + static_cast<uint64_t>(weights[w].rows) * cols;
+        if (a0 < lo || a0 + elements > hi || elements == 0) fail(kInvalidArgument, "A tile lies outside the weights.");
+        if (f.lane_stride >= (1u << 28)) fail(kLayoutLimit, "A fragment's lane stride exceeds 2^28.");
+        // under 2^32: check_matvec_group bounds the stacked elements
+        const uint64_t rel = first - lo + row_base[w] * cols;
+        const uint64_t span = (a0 - first + elements + V - 1) / V * V;   // lane bytes of the tile's vectors
+        const bool raw = f.kind == NZ_KIND_RAW;
+        nz_matvec_tile& r = out[t];
+        r.bits = raw ? f.bits + (first - origin) : f.bits + 8ull * tile.win0;
+        r.meta = raw ? 0 : f.meta + 2ull * tile.win0;
+        r.lanes = f.lanes + (first - origin);
+        r.counts = tile.counts;
+        r.head = static_cast<uint32_t>(a0 - first) | (f.lane_stride << 4);
+        r.row0 = static_cast<uint32_t>(rel / cols);
+        r.col0 = static_cast<uint32_t>(rel % cols);
+        // every byte the kernel's loads for this tile may reach
+        const bool ok = inside(r.lanes, span + (element_size == 4 ? 2ull * f.lane_stride : 0)) &&
+                        (raw ? inside(r.bits, span)
+                             : inside(r.bits, 8ull * windows + NZ_BITS_PAD) && inside(r.meta, 2ull * windows));
+        if (!ok) fail(kInvalidArgument, "A tile's data lies outside the packed buffer.");
+    }
+}
+
 namespace {
 
 // Maximal runs of one LUT and kind, their costs (elements, raw tiles at half

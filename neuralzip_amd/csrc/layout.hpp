@@ -82,6 +82,14 @@ void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
                  uint32_t n_weights, uint32_t cols, unsigned element_size, std::vector<uint32_t>& row_index,
                  std::vector<uint32_t>& entries);
 
+// One nz_matvec_tile per tile of a fused product over `weights` (the tiles
+// in launch order, as for plan_matvec): byte offsets checked against the
+// packed buffer's `store_bytes`, stacked row and column of each tile's first
+// vector, fragment indices checked against n_frags.
+void matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* tiles, uint32_t n_tiles,
+                  const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, unsigned element_size,
+                  uint64_t store_bytes, nz_matvec_tile* out);
+
 // CPU emulation of the decode kernel over a packed buffer; writes words
 // into `out` (the output workspace image).
 void emulate_decode(const uint8_t* base, const nz_frag_desc* frags, const nz_tile* tiles,

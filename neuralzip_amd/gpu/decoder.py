@@ -172,6 +172,8 @@ class HIPDecoder:
         tiles = np.concatenate([store.fragment_tiles(i) for i in order])
         weights = tuple((int(offset), int(rows)) for _, offset, rows in members)
         row_index, entries = _native.matvec_plan(store.descs, tiles, weights, cols, dtype.element_size)
+        # the kernel reads one record per tile (offsets, stacked row and column)
+        records = _native.matvec_tiles(store.descs, tiles, weights, cols, dtype.element_size, store.buffer.numel())
         device = store.device
         key = (dtype.element_size, bool(dtype.bit_reorder),
                any(store.descs[i]["kind"] == KIND_LONG for i in fragment_indices))
@@ -180,7 +182,7 @@ class HIPDecoder:
         segments = _native.plan_work(store.descs, tiles, slots)
         # one launch per kernel variant: segments of long-code fragments apart
         is_long = segments["kind"] == KIND_LONG
-        tensors = [torch.from_numpy(tiles.view(np.uint8).copy()).to(device),
+        tensors = [torch.from_numpy(records.view(np.uint8).copy()).to(device),
                    torch.from_numpy(row_index.view(np.uint8).copy()).to(device),
                    torch.from_numpy(entries.view(np.uint8).copy()).to(device)]
         launches = []
@@ -195,14 +197,14 @@ class HIPDecoder:
         bits = np.where(raw, numel, (descs["bit_length"].astype(np.int64) + 7) // 8)
         windows = np.where(raw, 0, (descs["bit_length"].astype(np.int64) + WINDOW_BITS - 1) // WINDOW_BITS)
         reads = int(bits.sum() + 2 * windows.sum() + (numel * (dtype.element_size - 1)).sum())
-        launch_weights, reduce_weights = _native.matvec_weights(weights), _native.matvec_weights(weights)
+        reduce_weights = _native.matvec_weights(weights)
         es, reorder = dtype.element_size, int(dtype.bit_reorder)
         launch_args = tuple((store.buffer.data_ptr(), store.frags.data_ptr(), tensors[0].data_ptr(), segments_ptr,
-                             n_segments, es, reorder, long_codes, ctypes.addressof(launch_weights), len(weights),
-                             int(cols)) for segments_ptr, n_segments, long_codes in launches)
+                             n_segments, es, reorder, long_codes, int(cols))
+                            for segments_ptr, n_segments, long_codes in launches)
         reduce_args = (tensors[1].data_ptr(), tensors[2].data_ptr(), ctypes.addressof(reduce_weights), len(weights))
         return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, weights, int(cols), len(tiles),
-                              store, tuple(launches), launch_weights, reads, reduce_weights, launch_args, reduce_args)
+                              store, tuple(launches), reads, reduce_weights, launch_args, reduce_args)
 
     def matvec(self, prepared, x, biases=None, partials=None, stream=None):
         """x @ W^T (+ bias) for each weight of the product: x is (batch, cols),
@@ -273,7 +275,7 @@ class PreparedMatvec:
     that share their input: their tiles (one launch per codebook kind) and
     the row index of the partial sums; output rows stacked in `weights`
     order."""
-    device_tensors: tuple = field(repr=False)          # tiles, row index, entries, segments on the device
+    device_tensors: tuple = field(repr=False)          # tile records, row index, entries, segments on the device
     device: torch.device
     layout: tuple                                      # (element_size, bit_reorder)
     dtype: torch.dtype
@@ -283,7 +285,6 @@ class PreparedMatvec:
     store: DeviceStore = field(repr=False)
     # (segments pointer, count, long_codes) of each launch
     launches: tuple = field(repr=False, default=())
-    launch_weights: object = field(repr=False, default=None)   # MatvecWeight array of the launches
     algorithmic_bytes: int = 0
     # MatvecWeight array of the reduce; each call sets its output and bias
     # pointers (so one plan serves one call at a time)

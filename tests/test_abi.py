@@ -23,7 +23,7 @@ def declared_functions():
 def test_header_declares_the_documented_entry_points():
     names = declared_functions()
     for expected in ("nz_last_error", "nz_abi_version", "nz_codebook_create", "nz_layout_encode", "nz_layout_pack",
-                     "nz_plan_work", "nz_plan_work_interleaved", "nz_decode_slots", "nz_decode_launch", "nz_matvec_plan", "nz_matvec_launch",
+                     "nz_plan_work", "nz_plan_work_interleaved", "nz_decode_slots", "nz_decode_launch", "nz_matvec_plan", "nz_matvec_tiles", "nz_matvec_launch",
                      "nz_matvec_reduce", "nz_storage_compress",
                      "nz_storage_decompress"):
         assert expected in names

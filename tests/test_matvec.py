@@ -1,5 +1,5 @@
 """Fused decode and matrix-vector product through the C ABI
-(nz_matvec_plan, nz_matvec_launch, nz_matvec_reduce).
+(nz_matvec_plan, nz_matvec_tiles, nz_matvec_launch, nz_matvec_reduce).
 
 The fused product has no counterpart in the reference, which always decodes
 a block's weights before the module's own GEMM (gpu/inference.py:379-509).
@@ -134,6 +134,65 @@ def test_plan_refuses_what_the_kernel_cannot_reduce():
         _native.matvec_plan(descs, tiles, [(offset, rows), (offset + cols, 1)], cols, 2)
 
 
+@pytest.mark.parametrize("case,dtype", [("huff0", torch.bfloat16), ("nzm1", torch.float16),
+                                        ("huff0", torch.float32)])
+def test_tile_records_place_each_tile_and_reach_its_own_bytes(case, dtype):
+    """nz_matvec_tiles against the weight itself: a record's stacked row and
+    column plus the elements of its first vector before the tile give the
+    tile's first element; the plan (computed from the tiles' element ranges,
+    not from the records) lists tile t under row0 (slot 0) and row0 + 1
+    (slot 1); and the bytes at the record's lane offsets (and, for a raw
+    chunk, at its exponent offset) are the weight's own lane bytes for the
+    tile's elements, split by the oracle."""
+    w, enc, offset = encoded_case(case, dtype)
+    base, descs, tiles = enc.host_image()
+    tiles = launch_order(descs, tiles)
+    rows, cols = w.shape
+    spec = DTYPES[dtype]
+    es, V = spec.element_size, 16 // spec.element_size
+    rec = _native.matvec_tiles(descs, tiles, [(offset, rows)], cols, es, len(base))
+    row_index, entries = _native.matvec_plan(descs, tiles, [(offset, rows)], cols, es)
+    a0, a1 = tile_spans(descs, tiles, offset)
+    head = rec["head"].astype(np.int64)
+    s0, stride = head & 15, head >> 4
+    assert ((a0 - s0) % V == 0).all() and (s0 < V).all()
+    assert (rec["row0"].astype(np.int64) * cols + rec["col0"] + s0 == a0).all() and (rec["col0"] < cols).all()
+    assert (rec["counts"] == tiles.view("<u4").reshape(-1, 4)[:, 3]).all()
+    assert (stride == descs["lane_stride"][tiles["frag"]]).all()
+    for r in range(rows):
+        for e in entries[row_index[r]:row_index[r + 1]]:
+            assert int(rec["row0"][int(e) // 2]) + int(e) % 2 == r
+    lanes = oracle.split_lanes(w.view(torch.uint8).numpy().tobytes(), es, spec.bit_reorder, spec.mantissa_bits,
+                               spec.exponent_mask.bit_length())
+    others = [k for k in range(es) if k != spec.selected_stream]
+    raw = descs["kind"][tiles["frag"]] == _native.KIND_RAW
+    assert raw.any() == (case == "huff0")
+    for t in range(len(tiles)):
+        lo, hi = int(a0[t]), int(a1[t])
+        for i, k in enumerate(others):
+            at = int(rec["lanes"][t]) + int(s0[t]) + i * int(stride[t])
+            assert np.array_equal(base[at:at + hi - lo], lanes[k][lo:hi])
+        if raw[t]:
+            at = int(rec["bits"][t]) + int(s0[t])
+            assert np.array_equal(base[at:at + hi - lo], lanes[spec.selected_stream][lo:hi])
+        else:
+            assert rec["meta"][t] == descs["meta"][tiles["frag"][t]] + 2 * tiles["win0"][t]
+
+
+def test_tile_records_refuse_what_the_kernel_must_not_read():
+    w, enc, offset = encoded_case("huff0", torch.bfloat16)
+    base, descs, tiles = enc.host_image()
+    rows, cols = w.shape
+    with pytest.raises(_native.NativeError, match="packed buffer"):
+        _native.matvec_tiles(descs, tiles, [(offset, rows)], cols, 2, len(base) // 2)
+    with pytest.raises(_native.NativeError, match="past the descriptors"):
+        _native.matvec_tiles(descs[:-1], tiles, [(offset, rows)], cols, 2, len(base))
+    with pytest.raises(_native.NativeError, match="outside the weights"):
+        _native.matvec_tiles(descs, tiles, [(offset, rows - 1)], cols, 2, len(base))
+    with pytest.raises(_native.NativeError, match="multiples"):
+        _native.matvec_tiles(descs, tiles, [(offset + 4, rows)], cols, 2, len(base))
+
+
 # ---------------------------------------------------------------- GPU parity
 
 def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2):
@@ -144,9 +203,10 @@ def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2
     device = torch.device("cuda:0")
     tiles = launch_order(descs, tiles)
     row_index, entries = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
+    records = _native.matvec_tiles(descs, tiles, weights, cols, spec.element_size, len(base))
     segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
     dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)
-    base_t, frags_t, tiles_t = dev(base), dev(descs), dev(tiles)
+    base_t, frags_t, tiles_t = dev(base), dev(descs), dev(records)
     index_t, entries_t = dev(row_index), dev(entries)
     launches = []
     for long_codes in (0, 1):
@@ -159,15 +219,14 @@ def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2
     bias_t = [None if b is None else b.to(device) for b in biases]
     partials = torch.empty(2 * len(tiles) * batch, dtype=torch.float32, device=device)
     stream = torch.cuda.current_stream(device).cuda_stream
-    launch_weights = _native.matvec_weights(weights)
     calls_out = []
     for _ in range(calls):
         partials.fill_(float("nan"))
         ys = [torch.full((batch, rows), float("nan"), dtype=dtype, device=device) for _, rows in weights]
         for seg_t, n, long_codes in launches:
             _native.matvec_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), seg_t.data_ptr(), n,
-                                  spec.element_size, spec.bit_reorder, long_codes, launch_weights, cols,
-                                  x_t.data_ptr(), batch, partials.data_ptr(), len(tiles), stream)
+                                  spec.element_size, spec.bit_reorder, long_codes, cols, x_t.data_ptr(), batch,
+                                  partials.data_ptr(), len(tiles), stream)
         outputs = _native.matvec_weights([(off, rows, y.data_ptr(), None if b is None else b.data_ptr())
                                           for (off, rows), y, b in zip(weights, ys, bias_t)])
         _native.matvec_reduce(index_t.data_ptr(), entries_t.data_ptr(), outputs, partials.data_ptr(), batch,

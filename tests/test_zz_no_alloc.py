@@ -19,9 +19,10 @@ def run_noalloc(base, descs, tiles, dtype, weights, cols, x, biases=None):
     device = torch.device("cuda:0")
     tiles = launch_order(descs, tiles)
     row_index, entries = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
+    records = _native.matvec_tiles(descs, tiles, weights, cols, spec.element_size, len(base))
     segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).copy()).to(device)
-    base_t, frags_t, tiles_t = dev(base), dev(descs), dev(tiles)
+    base_t, frags_t, tiles_t = dev(base), dev(descs), dev(records)
     index_t, entries_t = dev(row_index), dev(entries)
     is_long = segments["kind"] == _native.KIND_LONG
     short, long_ = segments[~is_long], segments[is_long]
