@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 8
+#define NZ_ABI_VERSION 9
 
 enum nz_status {
     NZ_OK = 0,
@@ -243,12 +243,13 @@ typedef struct {
 /* Row index of a fused product over the weights' tiles (n_tiles of them,
  * in launch order). Every element of every weight must be covered by
  * exactly one tile and each tile may touch at most two rows (cols of at
- * least 2048 guarantees it). Writes row_index[total_rows + 1] and
- * entries[row_index[n] .. row_index[n + 1]) = 2 * tile + slot (slot 1 when
- * the tile started in the previous row) for every stacked row n, in element
- * order. entries needs room for 2 * n_tiles values; *n_entries receives the
- * count. No counterpart in the reference, which decodes a block into its
- * workspace before the module's own GEMM reads it
+ * least 2048 guarantees it). The product's partial sums sit at positions
+ * that run row by row, each row's in element order: stacked row n's are
+ * positions row_index[n] .. row_index[n + 1], and entries[e] = 2 * tile +
+ * slot names the sum at position e (slot 1: the tile started in the
+ * previous row). entries needs room for 2 * n_tiles values; *n_entries
+ * receives the count. No counterpart in the reference, which decodes a
+ * block into its workspace before the module's own GEMM reads it
  * (gpu/inference.py:379-509). */
 int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles,
                    const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
@@ -256,22 +257,26 @@ int nz_matvec_plan(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_t
 
 /* The fused kernel's per-tile records of the same product (tiles and
  * weights as for nz_matvec_plan): out[t] holds tile t's byte offsets in the
- * packed buffer and the stacked output row and column of its first vector
- * (n_tiles records of 40 bytes, caller-allocated). Fails if a tile names a
- * fragment at or past n_frags, lies outside the weights, or would read
- * outside the packed buffer's store_bytes, so the kernel forms no address
- * the host has not checked. No counterpart in the reference (see
+ * packed buffer, the column of its first vector's first element and the
+ * partial position of its sum over its first row (nz_matvec_plan's
+ * positions; its sum over the next row, if it reaches it, is the next
+ * position). n_tiles records of 40 bytes, caller-allocated. Fails if a tile
+ * names a fragment at or past n_frags, lies outside the weights, or would
+ * read outside the packed buffer's store_bytes (so the kernel forms no
+ * address the host has not checked), or if the tiles do not cover the
+ * weights as nz_matvec_plan requires. No counterpart in the reference (see
  * nz_matvec_plan). */
 int nz_matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* tiles, uint32_t n_tiles,
                     const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, int element_size,
                     uint64_t store_bytes, nz_matvec_tile* out);
 
-/* Fused decode and product, first pass: for every tile t of the segments
+/* Fused decode and product, first pass: for every tile of the segments
  * (a plan of nz_plan_work over the same tiles), the products of its
  * elements with x (device, batch x cols in the weights' dtype, 1 <= batch
  * <= NZ_MATVEC_MAX_BATCH) summed per row they touch, in
- * partials[(2 * t + slot) * batch + b] (device fp32, 2 * n_tiles * batch
- * values). `tiles` is a device copy of nz_matvec_tiles' records for `base`
+ * partials[position * batch + b] (device fp32, room for 2 * n_tiles * batch
+ * values; positions as in nz_matvec_plan, from each tile's record). `tiles`
+ * is a device copy of nz_matvec_tiles' records for `base`
  * (the packed buffer they were checked against); `frags` gives each
  * segment's LUT. One call per codebook kind (long_codes) of the tiles.
  * Asynchronous on `stream`. No counterpart in the reference (see
@@ -281,13 +286,12 @@ int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_matve
                      uint32_t cols, const void* x, uint32_t batch, float* partials, uint32_t n_tiles, void* stream);
 
 /* Second pass: for each weight k and row n, weights[k].y[b * rows + n] =
- * (sum of the stacked row's partials, in entry order) + bias[n], rounded
- * once to the weights' dtype. row_index and entries are device copies of
- * nz_matvec_plan's output. Asynchronous on `stream`. No counterpart in the
+ * (sum of the stacked row's partials, in position order) + bias[n], rounded
+ * once to the weights' dtype. row_index is a device copy of
+ * nz_matvec_plan's. Asynchronous on `stream`. No counterpart in the
  * reference (see nz_matvec_plan). */
-int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
-                     uint32_t n_weights, const float* partials, uint32_t batch, int element_size, int bit_reorder,
-                     void* stream);
+int nz_matvec_reduce(const uint32_t* row_index, const nz_matvec_weight* weights, uint32_t n_weights,
+                     const float* partials, uint32_t batch, int element_size, int bit_reorder, void* stream);
 
 /* Bytes of partial sums the no-allocation product holds per GPU. */
 #define NZ_MATVEC_SCRATCH_BYTES (32u << 20)
@@ -296,7 +300,7 @@ int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const n
  * launches of nz_matvec_launch (short_segments, then long_segments, either
  * count may be 0) and nz_matvec_reduce, with the partial sums in a
  * library-owned device array of NZ_MATVEC_SCRATCH_BYTES per GPU instead of
- * a caller buffer; row_index / entries / weights[k].y / bias as for
+ * a caller buffer; row_index / weights[k].y / bias as for
  * nz_matvec_reduce. A product needing more than the array
  * (2 * n_tiles * batch * 4 bytes) fails with NZ_LAYOUT_LIMIT. Every call on
  * one GPU uses that GPU's array: calls that overlap on a GPU (on different
@@ -308,7 +312,7 @@ int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_matv
                       const nz_work* short_segments, uint32_t n_short, const nz_work* long_segments,
                       uint32_t n_long, int element_size, int bit_reorder, const nz_matvec_weight* weights,
                       uint32_t n_weights, uint32_t cols, const void* x, uint32_t batch, const uint32_t* row_index,
-                      const uint32_t* entries, void* stream);
+                      void* stream);
 
 /* ---- storage format (host codecs) -------------------------------------- */
 

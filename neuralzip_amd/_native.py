@@ -27,11 +27,11 @@ def tile_skip(tiles):
 
 
 WORK = np.dtype([("tile0", "<u4"), ("tile1", "<u4"), ("lut_frag", "<u4"), ("kind", "<u4")])
-# nz_matvec_tile: a fused product's tile with its offsets and stacked row and
-# column resolved (head = elements of the first vector before the tile |
-# lane stride << 4)
+# nz_matvec_tile: a fused product's tile with its offsets, first column and
+# first partial position resolved (head = elements of the first vector
+# before the tile | lane stride << 4)
 MATVEC_TILE = np.dtype([("bits", "<u8"), ("meta", "<u8"), ("lanes", "<u8"), ("counts", "<u4"), ("head", "<u4"),
-                        ("row0", "<u4"), ("col0", "<u4")])
+                        ("entry", "<u4"), ("col0", "<u4")])
 assert FRAG_DESC.itemsize == 64 and TILE.itemsize == 16 and WORK.itemsize == 16 and MATVEC_TILE.itemsize == 40
 
 KIND_RAW, KIND_SHORT, KIND_LONG = 0, 1, 2
@@ -70,7 +70,7 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 8
+ABI_VERSION = 9
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
@@ -114,9 +114,9 @@ def lib():
         L.nz_matvec_tiles.argtypes = [vp, u32, vp, u32, vp, u32, u32, ctypes.c_int, u64, vp]
         L.nz_matvec_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, u32, vp, u32,
                                        vp, u32, vp]
-        L.nz_matvec_reduce.argtypes = [vp, vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp]
+        L.nz_matvec_reduce.argtypes = [vp, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         L.nz_matvec_noalloc.argtypes = [vp, vp, vp, u32, vp, u32, vp, u32, ctypes.c_int, ctypes.c_int, vp, u32, u32,
-                                        vp, u32, vp, vp, vp]
+                                        vp, u32, vp, vp]
         L.nz_chunk_histograms.argtypes = [vp, u64, ctypes.POINTER(_LaneLayout), u64, ctypes.c_int, vp, vp]
         L.nz_clusterer_create.argtypes = [ctypes.c_double, ctypes.c_int, ctypes.POINTER(vp)]
         L.nz_clusterer_destroy.argtypes = [vp]
@@ -331,7 +331,9 @@ def matvec_weights(entries):
 def matvec_plan(descs, tiles, weights, cols, element_size):
     """(row_index uint32[total rows + 1], entries uint32[...]) of a fused
     product over `weights` ((workspace offset, rows) in increasing order)
-    whose elements the tiles cover exactly once."""
+    whose elements the tiles cover exactly once: row n's partial sums are
+    at positions row_index[n]..row_index[n + 1], and entries[e] = 2 * tile
+    + slot names the sum at position e."""
     array = matvec_weights(weights)
     row_index = np.zeros(sum(int(w[1]) for w in weights) + 1, dtype=np.uint32)
     entries = np.zeros(2 * max(len(tiles), 1), dtype=np.uint32)
@@ -346,7 +348,8 @@ def matvec_plan(descs, tiles, weights, cols, element_size):
 def matvec_tiles(descs, tiles, weights, cols, element_size, store_bytes):
     """The fused kernel's records (MATVEC_TILE, one per tile, in the tiles'
     order) of a product over `weights` ((workspace offset, rows) in
-    increasing order), checked against a packed buffer of store_bytes."""
+    increasing order), checked against a packed buffer of store_bytes;
+    `entry` is the tile's first partial position (matvec_plan's order)."""
     array = matvec_weights(weights)
     out = np.zeros(len(tiles), dtype=MATVEC_TILE)
     check(lib().nz_matvec_tiles(descs.ctypes.data, len(descs), tiles.ctypes.data if len(tiles) else None, len(tiles),
@@ -363,14 +366,14 @@ def matvec_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, elem
                                  int(n_tiles), stream_ptr))
 
 
-def matvec_reduce(row_index_ptr, entries_ptr, weights, partials_ptr, batch, element_size, bit_reorder, stream_ptr):
+def matvec_reduce(row_index_ptr, weights, partials_ptr, batch, element_size, bit_reorder, stream_ptr):
     """`weights`: a MatvecWeight array whose y (and bias) pointers are set."""
-    check(lib().nz_matvec_reduce(row_index_ptr, entries_ptr, ctypes.cast(weights, ctypes.c_void_p), len(weights),
-                                 partials_ptr, int(batch), int(element_size), int(bit_reorder), stream_ptr))
+    check(lib().nz_matvec_reduce(row_index_ptr, ctypes.cast(weights, ctypes.c_void_p), len(weights), partials_ptr,
+                                 int(batch), int(element_size), int(bit_reorder), stream_ptr))
 
 
 def matvec_noalloc(base_ptr, frags_ptr, tiles_ptr, n_tiles, short_ptr, n_short, long_ptr, n_long, element_size,
-                   bit_reorder, weights, cols, x_ptr, batch, row_index_ptr, entries_ptr, stream_ptr):
+                   bit_reorder, weights, cols, x_ptr, batch, row_index_ptr, stream_ptr):
     """Both passes of a fused product with the partial sums in the library's
     own per-device array (no allocation; 2 * n_tiles * batch * 4 bytes at
     most MATVEC_SCRATCH_BYTES). `weights`: a MatvecWeight array with y (and
@@ -378,7 +381,7 @@ def matvec_noalloc(base_ptr, frags_ptr, tiles_ptr, n_tiles, short_ptr, n_short, 
     check(lib().nz_matvec_noalloc(base_ptr, frags_ptr, tiles_ptr, int(n_tiles), short_ptr, int(n_short), long_ptr,
                                   int(n_long), int(element_size), int(bit_reorder),
                                   ctypes.cast(weights, ctypes.c_void_p), len(weights), int(cols), x_ptr, int(batch),
-                                  row_index_ptr, entries_ptr, stream_ptr))
+                                  row_index_ptr, stream_ptr))
 
 
 def chunk_histograms(words, spec, chunk_elements, *, threads=0, lane_counts=True):

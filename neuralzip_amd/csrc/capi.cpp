@@ -52,11 +52,11 @@ extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const 
                                      const void* short_segs, uint32_t n_short, const void* long_segs,
                                      uint32_t n_long, int element_size, int bit_reorder,
                                      const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols,
-                                     const void* x, uint32_t batch, const uint32_t* row_index,
-                                     const uint32_t* entries, void* stream, char* message, size_t message_size);
-extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
-                                    uint32_t n_weights, const float* partials, uint32_t batch, int element_size,
-                                    int bit_reorder, void* stream, char* message, size_t message_size);
+                                     const void* x, uint32_t batch, const uint32_t* row_index, void* stream,
+                                     char* message, size_t message_size);
+extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const nz_matvec_weight* weights, uint32_t n_weights,
+                                    const float* partials, uint32_t batch, int element_size, int bit_reorder,
+                                    void* stream, char* message, size_t message_size);
 
 extern "C" {
 
@@ -338,17 +338,16 @@ int nz_matvec_launch(const void* base, const nz_frag_desc* frags, const nz_matve
     return 0;
 }
 
-int nz_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
-                     uint32_t n_weights, const float* partials, uint32_t batch, int element_size, int bit_reorder,
-                     void* stream) {
-    if (!row_index || !entries || !partials || !weights) return set_error(nz::kInvalidArgument, "Null matvec reduce argument.");
+int nz_matvec_reduce(const uint32_t* row_index, const nz_matvec_weight* weights, uint32_t n_weights,
+                     const float* partials, uint32_t batch, int element_size, int bit_reorder, void* stream) {
+    if (!row_index || !partials || !weights) return set_error(nz::kInvalidArgument, "Null matvec reduce argument.");
     if (n_weights == 0 || n_weights > NZ_MATVEC_MAX_WEIGHTS)
         return set_error(nz::kInvalidArgument, "A fused product takes 1 to 4 weights.");
     if (batch > NZ_MATVEC_MAX_BATCH) return set_error(nz::kInvalidArgument, "matvec batch exceeds the maximum.");
     for (uint32_t k = 0; k < n_weights; ++k)
         if (!weights[k].y) return set_error(nz::kInvalidArgument, "Null matvec output.");
     char message[256] = {0};
-    const int rc = nz_hip_matvec_reduce(row_index, entries, weights, n_weights, partials, batch, element_size,
+    const int rc = nz_hip_matvec_reduce(row_index, weights, n_weights, partials, batch, element_size,
                                         bit_reorder, stream, message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
@@ -358,8 +357,8 @@ int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_matv
                       const nz_work* short_segments, uint32_t n_short, const nz_work* long_segments,
                       uint32_t n_long, int element_size, int bit_reorder, const nz_matvec_weight* weights,
                       uint32_t n_weights, uint32_t cols, const void* x, uint32_t batch, const uint32_t* row_index,
-                      const uint32_t* entries, void* stream) {
-    if (!base || !frags || !tiles || !x || !weights || !row_index || !entries || (n_short && !short_segments) ||
+                      void* stream) {
+    if (!base || !frags || !tiles || !x || !weights || !row_index || (n_short && !short_segments) ||
         (n_long && !long_segments))
         return set_error(nz::kInvalidArgument, "Null matvec argument.");
     const int rc0 = guarded([&] {
@@ -375,7 +374,7 @@ int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_matv
     char message[256] = {0};
     const int rc = nz_hip_matvec_noalloc(base, frags, tiles, n_tiles, short_segments, n_short, long_segments, n_long,
                                          element_size, bit_reorder, weights, n_weights, cols, x, batch, row_index,
-                                         entries, stream, message, sizeof message);
+                                         stream, message, sizeof message);
     if (rc) return set_error(rc, message);
     return 0;
 }

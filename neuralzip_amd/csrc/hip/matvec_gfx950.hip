@@ -99,16 +99,18 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Where a tile sits in the product: staging index i holds element
-// (row0 + (i >= split), col0 + i - (i >= split ? cols : 0)).
+// Where a tile sits in the product: staging index i holds column
+// col0 + i - (i >= split ? cols : 0) of the tile's first row (slot 0) or,
+// from `split` on, of the next row (slot 1); slot s's sum goes to partial
+// position entry + s.
 struct RowSpan {
-    uint32_t row0;
+    uint32_t entry;
     uint32_t col0;
     uint32_t split;   // staging index of the next row's first element
 };
 
 // Tile t's record (nz_matvec_tile, resolved and bounds-checked on the host):
-// its addresses in the packed buffer and its place in the stacked rows. One
+// its addresses in the packed buffer and its place in the product. One
 // 40-byte scalar load per tile; no fragment descriptor, weight lookup or
 // division on the device.
 template <int ES>
@@ -127,7 +129,7 @@ __device__ __forceinline__ TileInfo tile_record(const uint8_t* base, const nz_ma
     ti.s0 = r.head & 15u;
     ti.s1 = ti.s0 + nz_tile_elements(r.counts);
     ti.nv = (ti.s1 + V - 1) / V;
-    rs.row0 = r.row0;
+    rs.entry = r.entry;
     rs.col0 = r.col0;
     rs.split = cols - r.col0;
     return ti;
@@ -143,15 +145,19 @@ struct Partial {
 #pragma unroll
             for (int b = 0; b < BT; ++b) acc[s][b] = 0.0f;
     }
-    // Reduces over the wavefront; lane 63 writes the 2 x batch sums of tile
-    // `t` (every other lane's stores fall outside the buffer range).
-    __device__ __forceinline__ void flush(rsrc_t partials, uint32_t t, uint32_t batch, uint32_t lane) {
+    // Reduces over the wavefront; lane 63 writes the tile's sums to partial
+    // positions `entry` and, when the tile reaches the next row (`two`),
+    // entry + 1 (every other lane's stores fall outside the buffer range).
+    // Without `two`, position entry + 1 belongs to the next tile.
+    __device__ __forceinline__ void flush(rsrc_t partials, const RowSpan& rs, bool two, uint32_t batch,
+                                          uint32_t lane) {
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int b = 0; b < BT; ++b) {
+                if (s == 1 && !two) break;
                 const float total = wave_sum(acc[s][b]);
-                const uint32_t at = ((2 * t + s) * batch + b) * 4u;
+                const uint32_t at = ((rs.entry + s) * batch + b) * 4u;
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(total), partials,
                                                       lane == NZ_WAVE - 1 && b < static_cast<int>(batch) ? at : kOutOfRange,
                                                       0, 0);
@@ -262,7 +268,7 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_ma
         stage_tile<ES, LONG, ESC>(cur, fc, lut, stage, lane);
         p.clear();
         multiply_tile<ES, REORDER, LONG, BT>(cur, fc, stage, rs, x, cols, batch, lane, p, early);
-        p.flush(partials, seg.tile0 + t, batch, lane);
+        p.flush(partials, rs, rs.split < cur.s1, batch, lane);
         if (!more) break;
         t = tn;
         tn = after;
@@ -275,10 +281,10 @@ __device__ __forceinline__ void huffman_segment(const uint8_t* base, const nz_ma
 // A raw (uncoded) tile: the exponent lane is stored as is.
 template <int ES, bool REORDER, int BT>
 __device__ void raw_tile(const uint8_t* __restrict__ base, const nz_matvec_tile* tiles, uint32_t t, uint32_t cols,
-                         rsrc_t x, uint32_t batch, uint32_t lane, Partial<BT>& p) {
+                         rsrc_t x, uint32_t batch, uint32_t lane, Partial<BT>& p, RowSpan& rs, bool& two) {
     constexpr uint32_t V = 16 / ES;
-    RowSpan rs;
     const TileInfo ti = tile_record<ES>(base, tiles, t, cols, rs);
+    two = rs.split < ti.s1;
     const uint32_t s0 = ti.s0, s1 = ti.s1, nv = ti.nv, stride = ti.stride;
     for (uint32_t i = lane; i < nv; i += NZ_WAVE) {
         const uint32_t g = i * V;
@@ -353,8 +359,10 @@ void nz_matvec_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
         Partial<BT> p;
         for (uint32_t t = claim(&s_claim, lane); t < n; t = claim(&s_claim, lane)) {
             p.clear();
-            raw_tile<ES, REORDER, BT>(base, tiles, seg.tile0 + t, cols, x, batch, lane, p);
-            p.flush(partials, seg.tile0 + t, batch, lane);
+            RowSpan rs;
+            bool two;
+            raw_tile<ES, REORDER, BT>(base, tiles, seg.tile0 + t, cols, x, batch, lane, p, rs, two);
+            p.flush(partials, rs, two, batch, lane);
         }
         return;
     }
@@ -407,8 +415,8 @@ struct ReduceGroup {
 
 template <int ES, bool REORDER>
 __global__ __launch_bounds__(kReduceThreads)
-void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint32_t* __restrict__ entries,
-                             const float* __restrict__ partials, uint32_t batch, ReduceGroup g) {
+void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const float* __restrict__ partials,
+                             uint32_t batch, ReduceGroup g) {
     const uint32_t n = blockIdx.x * kReduceThreads + threadIdx.x;
     if (n >= g.total_rows) return;
     uint32_t w = 0;
@@ -422,13 +430,14 @@ void nz_matvec_reduce_kernel(const uint32_t* __restrict__ row_index, const uint3
                                                            : reinterpret_cast<const uint32_t*>(bias)[local]);
     const uint32_t e0 = row_index[n], e1 = row_index[n + 1];
     for (uint32_t b = 0; b < batch; ++b) {
-        // four entries' loads in flight at a time; the additions keep entry order
+        // the row's partial sums are adjacent; four loads in flight at a
+        // time, the additions in position (element) order
         float sum = 0.0f;
         for (uint32_t e = e0; e < e1; e += 4) {
             float part[4];
 #pragma unroll
             for (uint32_t k = 0; k < 4; ++k)
-                part[k] = e + k < e1 ? partials[entries[e + k] * batch + b] : 0.0f;
+                part[k] = e + k < e1 ? partials[(e + k) * batch + b] : 0.0f;
 #pragma unroll
             for (uint32_t k = 0; k < 4; ++k)
                 if (e + k < e1) sum += part[k];
@@ -500,7 +509,7 @@ extern "C" int nz_hip_matvec_launch(const void* base, const void* frags, const v
 
 // Row n of the stacked output: sum of its partial sums (+ its weight's bias),
 // rounded to the weight's dtype, into that weight's output.
-extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* entries, const nz_matvec_weight* weights,
+extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const nz_matvec_weight* weights,
                                     uint32_t n_weights, const float* partials, uint32_t batch, int element_size,
                                     int bit_reorder, void* stream, char* message, size_t message_size) {
     if (n_weights == 0 || batch == 0) return 0;
@@ -518,13 +527,13 @@ extern "C" int nz_hip_matvec_reduce(const uint32_t* row_index, const uint32_t* e
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid((g.total_rows + kReduceThreads - 1) / kReduceThreads);
     if (element_size == 2 && bit_reorder)
-        hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, true>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
+        hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, true>), grid, dim3(kReduceThreads), 0, st, row_index,
                            partials, batch, g);
     else if (element_size == 2)
-        hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, false>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
+        hipLaunchKernelGGL((nz_matvec_reduce_kernel<2, false>), grid, dim3(kReduceThreads), 0, st, row_index,
                            partials, batch, g);
     else
-        hipLaunchKernelGGL((nz_matvec_reduce_kernel<4, true>), grid, dim3(kReduceThreads), 0, st, row_index, entries,
+        hipLaunchKernelGGL((nz_matvec_reduce_kernel<4, true>), grid, dim3(kReduceThreads), 0, st, row_index,
                            partials, batch, g);
     const hipError_t rc = hipGetLastError();
     if (rc != hipSuccess) {
@@ -577,7 +586,7 @@ extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const 
                                      uint32_t n_long, int element_size, int bit_reorder,
                                      const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols,
                                      const void* x, uint32_t batch, const uint32_t* row_index,
-                                     const uint32_t* entries, void* stream, char* message, size_t message_size) {
+                                     void* stream, char* message, size_t message_size) {
     const uint64_t need = 2ull * n_tiles * batch * sizeof(float);
     if (need > NZ_MATVEC_SCRATCH_BYTES) {
         snprintf(message, message_size,
@@ -600,7 +609,7 @@ extern "C" int nz_hip_matvec_noalloc(const void* base, const void* frags, const 
         rc = nz_hip_matvec_launch(base, frags, tiles, long_segs, n_long, element_size, bit_reorder, 1, cols, x,
                                   batch, partials, n_tiles, stream, message, message_size);
     if (rc == 0)
-        rc = nz_hip_matvec_reduce(row_index, entries, weights, n_weights, partials, batch, element_size, bit_reorder,
+        rc = nz_hip_matvec_reduce(row_index, weights, n_weights, partials, batch, element_size, bit_reorder,
                                   stream, message, message_size);
     return rc;
 }

@@ -339,9 +339,14 @@ void matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* ti
     check_matvec_group(weights, n_weights, cols, element_size);
     const uint64_t V = 16 / element_size;
     std::vector<uint64_t> row_base(n_weights);
-    for (uint32_t k = 0, rows = 0; k < n_weights; rows += weights[k].rows, ++k) row_base[k] = rows;
+    uint64_t numel = 0;
+    for (uint32_t k = 0, rows = 0; k < n_weights; rows += weights[k].rows, ++k) {
+        row_base[k] = rows;
+        numel += static_cast<uint64_t>(weights[k].rows) * cols;
+    }
     // [offset, offset + bytes) inside the packed buffer
     auto inside = [&](uint64_t offset, uint64_t bytes) { return offset <= store_bytes && bytes <= store_bytes - offset; };
+    std::vector<std::pair<uint64_t, uint32_t>> order(n_tiles);   // (stacked first element, tile)
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const nz_tile& tile = tiles[t];
         if (tile.frag >= n_frags) fail(kInvalidArgument, "A tile names a fragment past the descriptors.");
@@ -349,15 +354,14 @@ void matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* ti
         const uint64_t a0 = f.out + tile.out0;
         const uint64_t first = a0 / V * V, origin = f.out / V * V;
         const uint32_t elements = nz_tile_elements(tile.counts), windows = nz_tile_windows(tile.counts);
-        // weight offsets are multiples of V, so `first` and a0 fall in the same weight
+        // weight offsets are multiples of V, so `first` and a0 fall in the same weight (and row)
         uint32_t w = 0;
         for (uint32_t k = 1; k < n_weights; ++k)
             if (first >= weights[k].offset) w = k;
         const uint64_t lo = weights[w].offset, hi = lo + static_cast<uint64_t>(weights[w].rows) * cols;
         if (a0 < lo || a0 + elements > hi || elements == 0) fail(kInvalidArgument, "A tile lies outside the weights.");
         if (f.lane_stride >= (1u << 28)) fail(kLayoutLimit, "A fragment's lane stride exceeds 2^28.");
-        // under 2^32: check_matvec_group bounds the stacked elements
-        const uint64_t rel = first - lo + row_base[w] * cols;
+        const uint64_t stacked = first - lo + row_base[w] * cols;   // under 2^32 (check_matvec_group)
         const uint64_t span = (a0 - first + elements + V - 1) / V * V;   // lane bytes of the tile's vectors
         const bool raw = f.kind == NZ_KIND_RAW;
         nz_matvec_tile& r = out[t];
@@ -366,14 +370,29 @@ void matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* ti
         r.lanes = f.lanes + (first - origin);
         r.counts = tile.counts;
         r.head = static_cast<uint32_t>(a0 - first) | (f.lane_stride << 4);
-        r.row0 = static_cast<uint32_t>(rel / cols);
-        r.col0 = static_cast<uint32_t>(rel % cols);
+        r.col0 = static_cast<uint32_t>(stacked % cols);
         // every byte the kernel's loads for this tile may reach
         const bool ok = inside(r.lanes, span + (element_size == 4 ? 2ull * f.lane_stride : 0)) &&
                         (raw ? inside(r.bits, span)
                              : inside(r.bits, 8ull * windows + NZ_BITS_PAD) && inside(r.meta, 2ull * windows));
         if (!ok) fail(kInvalidArgument, "A tile's data lies outside the packed buffer.");
+        order[t] = {stacked + (a0 - first), t};
     }
+    // Partial positions in element order: one per row a tile touches, so
+    // each row's sums are adjacent and in element order.
+    std::sort(order.begin(), order.end());
+    uint64_t cursor = 0;
+    uint32_t entry = 0;
+    for (const auto& [a0, t] : order) {
+        const uint64_t a1 = a0 + nz_tile_elements(tiles[t].counts);
+        if (a0 != cursor) fail(kInvalidArgument, "The tiles do not cover the weights exactly once.");
+        const uint64_t rows = (a1 - 1) / cols - a0 / cols;
+        if (rows > 1) fail(kLayoutLimit, "A tile spans more than two rows.");
+        out[t].entry = entry;
+        entry += 1 + static_cast<uint32_t>(rows);
+        cursor = a1;
+    }
+    if (cursor != numel) fail(kInvalidArgument, "The tiles do not cover the weights exactly once.");
 }
 
 namespace {

@@ -84,8 +84,9 @@ void plan_matvec(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
 
 // One nz_matvec_tile per tile of a fused product over `weights` (the tiles
 // in launch order, as for plan_matvec): byte offsets checked against the
-// packed buffer's `store_bytes`, stacked row and column of each tile's first
-// vector, fragment indices checked against n_frags.
+// packed buffer's `store_bytes`, the column of each tile's first vector and
+// its first partial position (plan_matvec's entry order), fragment indices
+// checked against n_frags; fails where plan_matvec would.
 void matvec_tiles(const nz_frag_desc* frags, uint32_t n_frags, const nz_tile* tiles, uint32_t n_tiles,
                   const nz_matvec_weight* weights, uint32_t n_weights, uint32_t cols, unsigned element_size,
                   uint64_t store_bytes, nz_matvec_tile* out);

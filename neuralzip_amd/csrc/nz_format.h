@@ -109,19 +109,23 @@ struct nz_work {                 // 16 bytes, one segment
 
 // One tile of a fused matrix-vector product with everything the kernel needs
 // resolved on the host (nz::matvec_tiles): its byte offsets in the packed
-// buffer and its place in the product's stacked output rows. The fused
-// kernel then reads one record per tile, with no fragment descriptor, no
-// weight lookup and no division. Staging index i of the tile (i counted from
-// its first vector's first element) holds element (row0 + (i >= cols - col0),
-// col0 + i - (i >= cols - col0 ? cols : 0)).
+// buffer and its place in the product's output. The fused kernel then reads
+// one record per tile, with no fragment descriptor, no weight lookup and no
+// division. Staging index i of the tile (i counted from its first vector's
+// first element) holds column col0 + i of the first vector's row for
+// i < cols - col0, and column i - (cols - col0) of the next row after it.
+// The tile's sum over its first row goes to partial position `entry`, its
+// sum over the next row (when it reaches it) to `entry` + 1: positions run
+// row by row, each row's in element order, so a row's partial sums are
+// adjacent.
 struct nz_matvec_tile {          // 40 bytes
     uint64_t bits;               // the tile's first window (raw tiles: the exponent lane at its first vector)
     uint64_t meta;               // its first window's metadata (raw tiles: 0)
     uint64_t lanes;              // raw lane 0 at its first vector
     uint32_t counts;             // as nz_tile
     uint32_t head;               // elements of the first vector before the tile | lane stride << 4
-    uint32_t row0;               // stacked output row and column of the first vector's first element
-    uint32_t col0;
+    uint32_t entry;              // partial position of the tile's sum over its first row
+    uint32_t col0;               // column of the first vector's first element
 };
 
 // Raw lanes and raw exponent lanes are stored with `out % V` leading pad

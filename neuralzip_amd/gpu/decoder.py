@@ -171,8 +171,8 @@ class HIPDecoder:
         order = sorted(fragment_indices, key=lambda i: (int(store.descs[i]["kind"]), int(store.descs[i]["lut"]), i))
         tiles = np.concatenate([store.fragment_tiles(i) for i in order])
         weights = tuple((int(offset), int(rows)) for _, offset, rows in members)
-        row_index, entries = _native.matvec_plan(store.descs, tiles, weights, cols, dtype.element_size)
-        # the kernel reads one record per tile (offsets, stacked row and column)
+        row_index, _ = _native.matvec_plan(store.descs, tiles, weights, cols, dtype.element_size)
+        # the kernel reads one record per tile (offsets, first column, partial position)
         records = _native.matvec_tiles(store.descs, tiles, weights, cols, dtype.element_size, store.buffer.numel())
         device = store.device
         key = (dtype.element_size, bool(dtype.bit_reorder),
@@ -183,8 +183,7 @@ class HIPDecoder:
         # one launch per kernel variant: segments of long-code fragments apart
         is_long = segments["kind"] == KIND_LONG
         tensors = [torch.from_numpy(records.view(np.uint8).copy()).to(device),
-                   torch.from_numpy(row_index.view(np.uint8).copy()).to(device),
-                   torch.from_numpy(entries.view(np.uint8).copy()).to(device)]
+                   torch.from_numpy(row_index.view(np.uint8).copy()).to(device)]
         launches = []
         for long_codes, group in enumerate((segments[~is_long], segments[is_long])):
             if len(group):
@@ -202,7 +201,7 @@ class HIPDecoder:
         launch_args = tuple((store.buffer.data_ptr(), store.frags.data_ptr(), tensors[0].data_ptr(), segments_ptr,
                              n_segments, es, reorder, long_codes, int(cols))
                             for segments_ptr, n_segments, long_codes in launches)
-        reduce_args = (tensors[1].data_ptr(), tensors[2].data_ptr(), ctypes.addressof(reduce_weights), len(weights))
+        reduce_args = (tensors[1].data_ptr(), ctypes.addressof(reduce_weights), len(weights))
         return PreparedMatvec(tuple(tensors), device, key[:2], dtype.torch_dtype, weights, int(cols), len(tiles),
                               store, tuple(launches), reads, reduce_weights, launch_args, reduce_args)
 
@@ -275,7 +274,7 @@ class PreparedMatvec:
     that share their input: their tiles (one launch per codebook kind) and
     the row index of the partial sums; output rows stacked in `weights`
     order."""
-    device_tensors: tuple = field(repr=False)          # tile records, row index, entries, segments on the device
+    device_tensors: tuple = field(repr=False)          # tile records, row index, segments on the device
     device: torch.device
     layout: tuple                                      # (element_size, bit_reorder)
     dtype: torch.dtype

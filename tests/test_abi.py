@@ -99,7 +99,7 @@ def test_no_alloc_product_refuses_more_partials_than_its_array():
     too_many_tiles = limit // (2 * 4 * 4) + 1
     rc = lib.nz_matvec_noalloc(dummy.ctypes.data, dummy.ctypes.data, dummy.ctypes.data, too_many_tiles,
                                dummy.ctypes.data, 1, None, 0, 2, 1, ctypes.addressof(weights), 1, 2048,
-                               dummy.ctypes.data, 4, dummy.ctypes.data, dummy.ctypes.data, None)
+                               dummy.ctypes.data, 4, dummy.ctypes.data, None)
     assert rc == -4 and b"no-allocation" in lib.nz_last_error()
 
 

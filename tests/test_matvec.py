@@ -137,13 +137,14 @@ def test_plan_refuses_what_the_kernel_cannot_reduce():
 @pytest.mark.parametrize("case,dtype", [("huff0", torch.bfloat16), ("nzm1", torch.float16),
                                         ("huff0", torch.float32)])
 def test_tile_records_place_each_tile_and_reach_its_own_bytes(case, dtype):
-    """nz_matvec_tiles against the weight itself: a record's stacked row and
-    column plus the elements of its first vector before the tile give the
-    tile's first element; the plan (computed from the tiles' element ranges,
-    not from the records) lists tile t under row0 (slot 0) and row0 + 1
-    (slot 1); and the bytes at the record's lane offsets (and, for a raw
-    chunk, at its exponent offset) are the weight's own lane bytes for the
-    tile's elements, split by the oracle."""
+    """nz_matvec_tiles against the weight itself: a record's column plus the
+    elements of its first vector before the tile give the tile's first
+    element's column; the plan (computed from the tiles' element ranges,
+    not from the records) names the record's partial position as the
+    tile's slot 0, and the next position as its slot 1 exactly when the
+    tile reaches the next row; and the bytes at the record's lane offsets
+    (and, for a raw chunk, at its exponent offset) are the weight's own lane
+    bytes for the tile's elements, split by the oracle."""
     w, enc, offset = encoded_case(case, dtype)
     base, descs, tiles = enc.host_image()
     tiles = launch_order(descs, tiles)
@@ -156,12 +157,14 @@ def test_tile_records_place_each_tile_and_reach_its_own_bytes(case, dtype):
     head = rec["head"].astype(np.int64)
     s0, stride = head & 15, head >> 4
     assert ((a0 - s0) % V == 0).all() and (s0 < V).all()
-    assert (rec["row0"].astype(np.int64) * cols + rec["col0"] + s0 == a0).all() and (rec["col0"] < cols).all()
+    assert (rec["col0"] + s0 == a0 % cols).all() and (rec["col0"] < cols).all()
     assert (rec["counts"] == tiles.view("<u4").reshape(-1, 4)[:, 3]).all()
     assert (stride == descs["lane_stride"][tiles["frag"]]).all()
-    for r in range(rows):
-        for e in entries[row_index[r]:row_index[r + 1]]:
-            assert int(rec["row0"][int(e) // 2]) + int(e) % 2 == r
+    entry = rec["entry"].astype(np.int64)
+    two = (a1 - 1) // cols > a0 // cols
+    assert (entries[entry] == 2 * np.arange(len(tiles))).all()
+    assert (entries[entry[two] + 1] == 2 * np.flatnonzero(two) + 1).all()
+    assert len(entries) == len(tiles) + two.sum() and row_index[-1] == len(entries)
     lanes = oracle.split_lanes(w.view(torch.uint8).numpy().tobytes(), es, spec.bit_reorder, spec.mantissa_bits,
                                spec.exponent_mask.bit_length())
     others = [k for k in range(es) if k != spec.selected_stream]
@@ -191,6 +194,10 @@ def test_tile_records_refuse_what_the_kernel_must_not_read():
         _native.matvec_tiles(descs, tiles, [(offset, rows - 1)], cols, 2, len(base))
     with pytest.raises(_native.NativeError, match="multiples"):
         _native.matvec_tiles(descs, tiles, [(offset + 4, rows)], cols, 2, len(base))
+    with pytest.raises(_native.NativeError, match="exactly once"):
+        _native.matvec_tiles(descs, np.delete(tiles, 5), [(offset, rows)], cols, 2, len(base))
+    with pytest.raises(_native.NativeError, match="more than two rows"):
+        _native.matvec_tiles(descs, tiles, [(offset, rows * 4)], cols // 4, 2, len(base))
 
 
 # ---------------------------------------------------------------- GPU parity
@@ -202,12 +209,12 @@ def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2
     spec = DTYPES[dtype]
     device = torch.device("cuda:0")
     tiles = launch_order(descs, tiles)
-    row_index, entries = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
+    row_index, _ = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
     records = _native.matvec_tiles(descs, tiles, weights, cols, spec.element_size, len(base))
     segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
     dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)
     base_t, frags_t, tiles_t = dev(base), dev(descs), dev(records)
-    index_t, entries_t = dev(row_index), dev(entries)
+    index_t = dev(row_index)
     launches = []
     for long_codes in (0, 1):
         sel = segments[(segments["kind"] == _native.KIND_LONG) == bool(long_codes)]
@@ -229,8 +236,8 @@ def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2
                                   partials.data_ptr(), len(tiles), stream)
         outputs = _native.matvec_weights([(off, rows, y.data_ptr(), None if b is None else b.data_ptr())
                                           for (off, rows), y, b in zip(weights, ys, bias_t)])
-        _native.matvec_reduce(index_t.data_ptr(), entries_t.data_ptr(), outputs, partials.data_ptr(), batch,
-                              spec.element_size, spec.bit_reorder, stream)
+        _native.matvec_reduce(index_t.data_ptr(), outputs, partials.data_ptr(), batch, spec.element_size,
+                              spec.bit_reorder, stream)
         torch.cuda.synchronize(device)
         calls_out.append([y.cpu() for y in ys])
     return calls_out

@@ -18,12 +18,12 @@ def run_noalloc(base, descs, tiles, dtype, weights, cols, x, biases=None):
     spec = DTYPES[dtype]
     device = torch.device("cuda:0")
     tiles = launch_order(descs, tiles)
-    row_index, entries = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
+    row_index, _ = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
     records = _native.matvec_tiles(descs, tiles, weights, cols, spec.element_size, len(base))
     segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).copy()).to(device)
     base_t, frags_t, tiles_t = dev(base), dev(descs), dev(records)
-    index_t, entries_t = dev(row_index), dev(entries)
+    index_t = dev(row_index)
     is_long = segments["kind"] == _native.KIND_LONG
     short, long_ = segments[~is_long], segments[is_long]
     short_t = dev(short) if len(short) else None
@@ -39,8 +39,7 @@ def run_noalloc(base, descs, tiles, dtype, weights, cols, x, biases=None):
     _native.matvec_noalloc(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), len(tiles),
                            None if short_t is None else short_t.data_ptr(), len(short),
                            None if long_t is None else long_t.data_ptr(), len(long_), spec.element_size,
-                           spec.bit_reorder, outputs, cols, x_t.data_ptr(), batch, index_t.data_ptr(),
-                           entries_t.data_ptr(), stream)
+                           spec.bit_reorder, outputs, cols, x_t.data_ptr(), batch, index_t.data_ptr(), stream)
     torch.cuda.synchronize(device)
     return [y.cpu() for y in ys]
 
