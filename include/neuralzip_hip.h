@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 9
+#define NZ_ABI_VERSION 10
 
 enum nz_status {
     NZ_OK = 0,
@@ -126,12 +126,17 @@ int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base,
  * range of one LUT and kind) per workgroup. Maximal runs of one LUT and kind
  * share out `slots` workgroups (the number the device runs at once, from
  * nz_decode_slots; at least one per run, at most one per 16 tiles) in
- * proportion to their elements and
- * are cut into that many segments of about equal elements. With
- * segments == NULL only *n_segments is set.
+ * proportion to their elements and are cut into that many segments of about
+ * equal elements. first_weight (1 to 16; 1 = equal segments) is for a
+ * device that runs two workgroups per compute unit: when the segments fill
+ * all `slots` and are of one kernel variant (no long-code runs beside
+ * others), segments 0 .. slots/2 - 1, whose workgroups are dispatched first
+ * and win issue arbitration against the one sharing their unit, get
+ * first_weight times the elements of the others. With segments == NULL only
+ * *n_segments is set.
  * Replaces: the block->group / block->local id tensors (decoder.py:168-179). */
 int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
-                 nz_work* segments, uint32_t capacity, uint32_t* n_segments);
+                 double first_weight, nz_work* segments, uint32_t capacity, uint32_t* n_segments);
 
 /* The decode launch's plan: the same shares of workgroups as nz_plan_work,
  * but each run's tiles are dealt round-robin to its segments: each segment

@@ -70,7 +70,7 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 9
+ABI_VERSION = 10
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
@@ -101,7 +101,7 @@ def lib():
         L.nz_layout_totals_get.argtypes = [vp, ctypes.POINTER(_Totals)]
         L.nz_layout_fragment_info.argtypes = [vp, sz, ctypes.POINTER(_FragmentInfo)]
         L.nz_layout_pack.argtypes = [vp, vp, u64, vp, u32, vp, vp]
-        L.nz_plan_work.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32)]
+        L.nz_plan_work.argtypes = [vp, vp, u32, u32, ctypes.c_double, vp, u32, ctypes.POINTER(u32)]
         L.nz_plan_work_interleaved.argtypes = [vp, vp, u32, u32, vp, u32, ctypes.POINTER(u32), vp]
         L.nz_decode_slots.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.nz_decode_launch.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
@@ -225,14 +225,17 @@ class Layout:
         return descs, tiles
 
 
-def plan_work(descs, tiles, slots):
-    """The launch's segments (WORK records), one per workgroup."""
+def plan_work(descs, tiles, slots, first_weight=1.0):
+    """The launch's segments (WORK records), one per workgroup; with
+    first_weight > 1 the first slots / 2 get that many times the elements
+    when the segments fill every slot (see nz_plan_work)."""
     n = ctypes.c_uint32()
     tp = tiles.ctypes.data if len(tiles) else None
-    check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), None, 0, ctypes.byref(n)))
-    segments = np.zeros(n.value, dtype=WORK)
-    check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), segments.ctypes.data, n.value,
+    check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), float(first_weight), None, 0,
                              ctypes.byref(n)))
+    segments = np.zeros(n.value, dtype=WORK)
+    check(lib().nz_plan_work(descs.ctypes.data, tp, len(tiles), int(slots), float(first_weight),
+                             segments.ctypes.data, n.value, ctypes.byref(n)))
     return segments
 
 

@@ -190,10 +190,10 @@ int nz_layout_pack(const nz_layout* layout, uint8_t* dst, uint64_t dst_base, con
 }
 
 int nz_plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
-                 nz_work* segments, uint32_t capacity, uint32_t* n_segments) {
+                 double first_weight, nz_work* segments, uint32_t capacity, uint32_t* n_segments) {
     return guarded([&] {
         if (!frags || (!tiles && n_tiles) || !n_segments) nz::fail(nz::kInvalidArgument, "Null plan argument.");
-        const auto plan = nz::plan_work(frags, tiles, n_tiles, slots);
+        const auto plan = nz::plan_work(frags, tiles, n_tiles, slots, first_weight);
         *n_segments = static_cast<uint32_t>(plan.size());
         if (segments) {
             if (plan.size() > capacity) nz::fail(nz::kInvalidArgument, "Segment buffer is too small.");

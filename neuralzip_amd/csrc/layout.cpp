@@ -457,25 +457,46 @@ Shares share_out(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_til
 
 }  // namespace
 
-std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots) {
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
+                               double first_weight) {
+    if (!(first_weight >= 1.0 && first_weight <= 16.0)) fail(kInvalidArgument, "first_weight must be in [1, 16].");
     const Shares sh = share_out(frags, tiles, n_tiles, slots);
     const std::vector<nz_work>& runs = sh.runs;
     const std::vector<double>& cost = sh.cost;
     const std::vector<uint64_t>& share = sh.share;
     const size_t n_seg = runs.size();
-    // Cut each run into its share of ranges of about equal cost.
+    // Segment b runs as workgroup b. With two workgroups per compute unit and
+    // the device full (one segment per slot), workgroups b < slots / 2 are
+    // dispatched first and each shares its unit with one dispatched later;
+    // the older one's waves win issue arbitration and it runs faster, so it
+    // gets first_weight times the cost. Only for a launch of one kernel
+    // variant: long-code runs are launched apart from the others.
+    uint64_t total = 0;
+    bool any_long = false, any_other = false;
+    for (size_t i = 0; i < n_seg; ++i) {
+        total += std::min<uint64_t>(share[i], runs[i].tile1 - runs[i].tile0);
+        (runs[i].kind == NZ_KIND_LONG ? any_long : any_other) = true;
+    }
+    const bool paired = first_weight != 1.0 && total == slots && slots % 2 == 0 && !(any_long && any_other);
+    auto weight = [&](uint64_t b) { return paired && b < slots / 2 ? first_weight : 1.0; };
+    // Cut each run into its share of ranges of about equal weighted cost.
     std::vector<nz_work> ranges;
     for (size_t i = 0; i < n_seg; ++i) {
         const nz_work& run = runs[i];
         const uint64_t parts = std::min<uint64_t>(share[i], run.tile1 - run.tile0);
-        double acc = 0;
+        const uint64_t base = ranges.size();
+        double weights = 0;
+        for (uint64_t j = 0; j < parts; ++j) weights += weight(base + j);
+        double acc = 0, reached = weight(base);   // weight of the segments up to the current one
         uint32_t begin = run.tile0;
         uint64_t made = 0;
         for (uint32_t t = run.tile0; t < run.tile1; ++t) {
             const double n = nz_tile_elements(tiles[t].counts);
             acc += frags[tiles[t].frag].kind == NZ_KIND_RAW ? 0.5 * n : n;
             const bool last = t + 1 == run.tile1;
-            if (last || (made + 1 < parts && acc >= cost[i] * (made + 1) / parts && run.tile1 - (t + 1) >= parts - made - 1)) {
+            if (last || (made + 1 < parts && acc >= cost[i] * reached / weights &&
+                         run.tile1 - (t + 1) >= parts - made - 1)) {
+                if (!last) reached += weight(base + made + 1);
                 ranges.push_back({begin, t + 1, tiles[begin].frag, run.kind});
                 begin = t + 1;
                 ++made;

@@ -56,8 +56,12 @@ void pack_fragment(const Fragment& f, uint8_t* dst, uint64_t offset, uint64_t lu
 // LUT and kind share out `slots` workgroups (the number the device runs at
 // once; at least one per run, and no more than one per 16 tiles) in
 // proportion to their elements, and each run is cut into that many
-// contiguous segments of about equal elements.
-std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots);
+// contiguous segments of about equal elements -- or, when the segments fill
+// all `slots` (two workgroups per compute unit) and the launch is of one
+// kernel variant, with segments b < slots / 2 (dispatched first) weighted
+// first_weight to the others' 1.
+std::vector<nz_work> plan_work(const nz_frag_desc* frags, const nz_tile* tiles, uint32_t n_tiles, uint32_t slots,
+                               double first_weight = 1.0);
 
 // The same shares, with each run's tiles dealt round-robin to its segments:
 // each segment of a run of P segments takes the run's tiles r, r + P,

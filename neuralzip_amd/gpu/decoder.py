@@ -21,6 +21,12 @@ WINDOW_BITS = 64
 # runs at once (two 16-wavefront workgroups per CU on MI355X, 512 in all), so
 # that one round of equal-work workgroups covers the launch.
 SLOTS = None
+# Fused products: elements of a workgroup dispatched first against one
+# dispatched later on the same compute unit. The first wins issue
+# arbitration; with equal segments it finished its tiles in 70 % of the
+# time of the second (Llama-3-8B shapes), and the second then ran alone.
+# 1.75 evened them out best of 1.5, 1.75, 2 and 2.5.
+MATVEC_FIRST_WEIGHT = 1.75
 
 
 def _align(value, alignment=256):
@@ -157,7 +163,7 @@ class HIPDecoder:
                 cache[(device, key)] = _native.decode_slots(*key)
         return cache[(device, key)]
 
-    def prepare_matvec(self, store, members, dtype, cols, slots=SLOTS):
+    def prepare_matvec(self, store, members, dtype, cols, slots=SLOTS, first_weight=MATVEC_FIRST_WEIGHT):
         """Fused product over `members`, (fragment indices, workspace offset,
         rows) of weights with `cols` columns that share their input. Raises
         NativeError when the tiles do not suit the fused kernel (rows shorter
@@ -179,7 +185,7 @@ class HIPDecoder:
                any(store.descs[i]["kind"] == KIND_LONG for i in fragment_indices))
         if slots is None:
             slots = self.slots(device, key)
-        segments = _native.plan_work(store.descs, tiles, slots)
+        segments = _native.plan_work(store.descs, tiles, slots, first_weight)
         # one launch per kernel variant: segments of long-code fragments apart
         is_long = segments["kind"] == KIND_LONG
         tensors = [torch.from_numpy(records.view(np.uint8).copy()).to(device),

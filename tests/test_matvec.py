@@ -134,6 +134,45 @@ def test_plan_refuses_what_the_kernel_cannot_reduce():
         _native.matvec_plan(descs, tiles, [(offset, rows), (offset + cols, 1)], cols, 2)
 
 
+def synthetic_tiles(kinds, n_tiles, elements=1000):
+    """Descriptors and tiles of one fragment per kind (n_tiles each): enough
+    for the planner, which reads kinds, LUT offsets and element counts."""
+    descs = np.zeros(len(kinds), dtype=_native.FRAG_DESC)
+    descs["kind"] = kinds
+    descs["lut"] = np.arange(len(kinds)) * 4096
+    tiles = np.zeros(n_tiles * len(kinds), dtype=_native.TILE)
+    tiles["frag"] = np.repeat(np.arange(len(kinds)), n_tiles)
+    tiles["n_out"] = elements
+    return descs, tiles
+
+
+def test_plan_weights_the_workgroups_dispatched_first():
+    """nz_plan_work's first_weight: when the segments fill every slot, the
+    first half (dispatched first) gets that many times the elements of the
+    second half, the segments still cover every tile once in order, and
+    otherwise (fewer segments than slots, or long-code runs beside others)
+    the segments stay equal."""
+    descs, tiles = synthetic_tiles([_native.KIND_SHORT], 20000)
+    even = _native.plan_work(descs, tiles, 512)
+    weighted = _native.plan_work(descs, tiles, 512, 1.75)
+    for plan in (even, weighted):
+        assert len(plan) == 512 and plan["tile0"][0] == 0 and plan["tile1"][-1] == len(tiles)
+        assert (plan["tile0"][1:] == plan["tile1"][:-1]).all()
+    sizes = (weighted["tile1"] - weighted["tile0"]).astype(np.float64)
+    assert abs(sizes[:256].mean() / sizes[256:].mean() - 1.75) < 0.02
+    assert np.ptp(even["tile1"] - even["tile0"]) <= 1
+    # fewer segments than slots (16 tiles per workgroup at least): equal
+    descs, tiles = synthetic_tiles([_native.KIND_SHORT], 4000)
+    plan = _native.plan_work(descs, tiles, 512, 1.75)
+    assert len(plan) == 250 and np.ptp(plan["tile1"] - plan["tile0"]) <= 1
+    # short and long runs in one plan become two launches: equal
+    descs, tiles = synthetic_tiles([_native.KIND_SHORT, _native.KIND_LONG], 10000)
+    plan = _native.plan_work(descs, tiles, 512, 1.75)
+    assert len(plan) == 512 and np.ptp(plan["tile1"] - plan["tile0"]) <= 1
+    with pytest.raises(_native.NativeError, match="first_weight"):
+        _native.plan_work(descs, tiles, 512, 0.5)
+
+
 @pytest.mark.parametrize("case,dtype", [("huff0", torch.bfloat16), ("nzm1", torch.float16),
                                         ("huff0", torch.float32)])
 def test_tile_records_place_each_tile_and_reach_its_own_bytes(case, dtype):
@@ -202,7 +241,7 @@ def test_tile_records_refuse_what_the_kernel_must_not_read():
 
 # ---------------------------------------------------------------- GPU parity
 
-def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2):
+def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2, first_weight=1.0):
     """Outputs (one per weight) of `calls` consecutive calls of one fused
     product over `weights` ((workspace offset, rows) in increasing order),
     with the partials and outputs poisoned before each call."""
@@ -211,7 +250,8 @@ def run_matvec(base, descs, tiles, dtype, weights, cols, x, biases=None, calls=2
     tiles = launch_order(descs, tiles)
     row_index, _ = _native.matvec_plan(descs, tiles, weights, cols, spec.element_size)
     records = _native.matvec_tiles(descs, tiles, weights, cols, spec.element_size, len(base))
-    segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0))
+    segments = _native.plan_work(descs, tiles, _native.decode_slots(spec.element_size, spec.bit_reorder, 0),
+                                 first_weight)
     dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)
     base_t, frags_t, tiles_t = dev(base), dev(descs), dev(records)
     index_t = dev(row_index)
@@ -253,6 +293,28 @@ def check_product(y, w, x, bias, dtype):
     assert np.isfinite(got).all()
     err = np.abs(got - ref)
     assert (err <= tol).all(), f"max error {err.max():.3g}, worst ratio {(err / tol).max():.3g}"
+
+
+@pytest.mark.gpu
+def test_weighted_plan_gives_the_same_bits():
+    """A product large enough to fill every workgroup slot (about 11,400
+    tiles): the runtime's plan, whose first-dispatched workgroups take 1.75
+    times the elements of the others, gives the bits of the equal plan,
+    within the exact product's bound."""
+    from neuralzip_amd.gpu.decoder import MATVEC_FIRST_WEIGHT
+    w = random_weight(torch.bfloat16, 4096, 4096, 9)
+    raw = w.view(torch.uint8).numpy().reshape(-1).copy()
+    books = {0: _native.Codebook(singleton_header(raw, torch.bfloat16))}
+    enc = Encoded([(raw, torch.bfloat16, 131072, [0] * (w.numel() // 131072), 64)], books)
+    base, descs, tiles = enc.host_image()
+    slots = _native.decode_slots(2, 1, 0)
+    assert len(_native.plan_work(descs, launch_order(descs, tiles), slots, MATVEC_FIRST_WEIGHT)) == slots
+    x = torch.randn(2, 4096, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    (even,), _ = run_matvec(base, descs, tiles, torch.bfloat16, [(64, 4096)], 4096, x)
+    (weighted,), _ = run_matvec(base, descs, tiles, torch.bfloat16, [(64, 4096)], 4096, x,
+                                first_weight=MATVEC_FIRST_WEIGHT)
+    assert torch.equal(weighted.view(torch.int16), even.view(torch.int16))
+    check_product(weighted, w, x, None, torch.bfloat16)
 
 
 @pytest.mark.gpu
