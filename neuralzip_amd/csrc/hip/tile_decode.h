@@ -332,12 +332,11 @@ __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, L
         do {
             const uint2 e = lut_step<LONG, ESC>(lut, w0, w1, w2, w3);
             uint32_t* dst = reinterpret_cast<uint32_t*>(stage) + __builtin_amdgcn_ubfe(bit, 5u, 27u);
-            // The entry's bytes in this dword, and the ones past it. The bit
-            // field extract reads the low five bits of its offset and width,
-            // so this is ubfe(e.y, 32 - fill, fill) with fill = bit % 32: the
-            // top `fill` bits, none when fill is 0.
-            const uint32_t low = e.y << (bit & 31u);
-            const uint32_t high = __builtin_amdgcn_ubfe(e.y, 0u - bit, bit);
+            // The entry's bytes in this dword, and the ones past it: one
+            // 64-bit shift (two 32-bit shifts and a negation before).
+            const uint64_t both = static_cast<uint64_t>(e.y) << (bit & 31u);
+            const uint32_t low = static_cast<uint32_t>(both);
+            const uint32_t high = static_cast<uint32_t>(both >> 32);
             __hip_atomic_fetch_or(dst, low, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             __hip_atomic_fetch_or(dst + 1, high, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             // The ORs complete before the wavefront issues its next LDS
