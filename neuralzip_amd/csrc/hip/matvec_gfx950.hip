@@ -4,8 +4,9 @@
 // weights W (rows x cols each) that share the activations x, stored in the
 // layout of nz_format.h, without writing W anywhere. The weights' rows are
 // stacked in workspace order; each tile's record (nz_matvec_tile, resolved
-// on the host) gives its addresses and its stacked row and column. No
-// counterpart in the reference, which always decodes a block
+// on the host) gives its addresses, its first column and the positions of
+// its partial sums. No counterpart in the reference, which always decodes a
+// block
 // into its workspace before the module's own GEMM reads it
 // (neuralzip/gpu/inference.py:379-509).
 //
@@ -17,8 +18,9 @@
 //     most 2048 elements, so with cols >= 2048 it touches at most two rows;
 //     the wavefront writes one partial sum per (row slot, activation row).
 //   * nz_matvec_reduce_kernel: one thread per output row adds the row's
-//     partial sums in element order (a host-built CSR index), adds the bias
-//     in fp32 and rounds once to the weight's dtype.
+//     partial sums, which sit at adjacent positions in element order (a
+//     host-built row index), adds the bias in fp32 and rounds once to the
+//     weight's dtype.
 // Both kernels fix the order of every addition, so repeated calls give
 // identical bits.
 #include <hip/hip_runtime.h>
