@@ -6,8 +6,7 @@
 // stacked in workspace order; each tile's record (nz_matvec_tile, resolved
 // on the host) gives its addresses, its first column and the positions of
 // its partial sums. No counterpart in the reference, which always decodes a
-// block
-// into its workspace before the module's own GEMM reads it
+// block into its workspace before the module's own GEMM reads it
 // (neuralzip/gpu/inference.py:379-509).
 //
 //   * nz_matvec_kernel: the decode kernel's work split (one workgroup per
