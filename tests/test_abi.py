@@ -123,3 +123,35 @@ def test_decode_args_layout_and_schedule_checks():
     assert lib.nz_decode_schedule(bad, 1, None, 0, None, None, None, None, None) == -1
     assert b"reserved" in lib.nz_last_error()
     assert lib.nz_decode_schedule(None, 0, None, 0, None, None, None, None, None) == 0
+
+
+def test_numpy_records_match_the_device_structs():
+    """The numpy mirrors of the device records (FRAG_DESC, TILE, WORK,
+    MATVEC_TILE) have the field names, sizes and offsets of the structs in
+    nz_format.h, computed from their declarations (uint64_t / uint32_t /
+    uint16_t fields, natural alignment)."""
+    text = (ROOT / "neuralzip_amd" / "csrc" / "nz_format.h").read_text()
+    width = {"uint64_t": 8, "uint32_t": 4, "uint16_t": 2}
+
+    def layout(name):
+        body = re.search(rf"struct {name} \{{(.*?)\}};", text, re.S).group(1)
+        fields = re.findall(r"(uint\d+_t)\s+([\w\s,]+);", re.sub(r"//.*", "", body))
+        out, offset = [], 0
+        for kind, names in fields:
+            for n in (x.strip() for x in names.split(",")):
+                size = width[kind]
+                offset = (offset + size - 1) // size * size
+                out.append((n, offset, size))
+                offset += size
+        return out, (offset + 7) // 8 * 8 if any(s == 8 for _, _, s in out) else offset
+
+    for name, dtype in (("nz_frag_desc", _native.FRAG_DESC), ("nz_work", _native.WORK),
+                        ("nz_matvec_tile", _native.MATVEC_TILE)):
+        fields, size = layout(name)
+        assert dtype.itemsize == size, name
+        assert [(n, dtype.fields[n][1], dtype.fields[n][0].itemsize) for n in dtype.names] == fields, name
+    # nz_tile's last word is split in two 16-bit halves on the numpy side
+    fields, size = layout("nz_tile")
+    assert _native.TILE.itemsize == size == 16
+    assert [n for n, _, _ in fields] == ["frag", "win0", "out0", "counts"]
+    assert _native.TILE.fields["shape"][1] == 12 and _native.TILE.fields["n_out"][1] == 14
