@@ -324,8 +324,10 @@ int nz_matvec_noalloc(const void* base, const nz_frag_desc* frags, const nz_matv
 /* Huff0 tree description for a 256-bin histogram plus `prior_count` per
  * symbol, code lengths limited to max_bits (<= 12). With header == NULL only
  * *header_size is set. Replaces: _huff0_cpp.build_codebook_from_counts
- * (binding_helpers.h:9-83 -> codebooks.h:1-42). Byte equality with Zstd's
- * table construction is not claimed; the description is format-valid. */
+ * (binding_helpers.h:9-83 -> codebooks.h:1-42): the counts are scaled as
+ * there, and the lengths and bytes are those of Zstd's HUF_buildCTable_wksp
+ * and HUF_writeCTable_wksp, which the reference calls. Fails like them when
+ * more than 128 weights do not FSE-compress below half their count. */
 int nz_huff0_build(const uint64_t* counts256, uint32_t prior_count, uint32_t max_bits,
                    uint8_t* header, size_t capacity, size_t* header_size);
 

@@ -4,14 +4,13 @@
 // 4-stream block (Zstd's format, RFC 8878 4.2) or an NZM1 frame
 // (neuralzip/native/mixed_huffman.h:117-240). This file provides:
 //   * Huff0 tables from histograms (binding_helpers.h:9-83, codebooks.h:1-42):
-//     counts are scaled like the reference, lengths are limited to max_bits
-//     with the adjustment of ITU-T T.81 Annex K.3, and the tree description
-//     is written with FSE-compressed or 4-bit weights;
+//     counts are scaled like the reference, then code lengths and the tree
+//     description come from the steps of Zstd's HUF_buildCTable_wksp and
+//     HUF_writeCTable_wksp, which the reference calls, so that both are the
+//     reference's bytes;
 //   * Huff0 4X and NZM1 frame encoders and decoders;
 //   * the threaded direct-storage encoder (direct_storage.h:72-214) and the
 //     aligned-chunk decoder (decode_queue.h:1-113).
-// Zstd's exact bytes are not reproduced: the encoders emit format-valid
-// streams whose decoding is pinned; the code lengths may differ.
 #include <algorithm>
 #include <atomic>
 #include <cstring>
@@ -27,49 +26,184 @@ namespace {
 int highbit(uint32_t v) { return 31 - __builtin_clz(v); }
 
 // --------------------------------------------------------------- Huffman
-// Optimal code lengths limited to `max_bits` (package-merge, Larmore and
-// Hirschberg 1990), in its counting form: each level keeps only whether the
-// merged items are leaves or packages; the backtrack from the top level
-// takes 2n-2 items, credits one bit to the cheapest `leaves` symbols and
-// descends into twice as many items for every package taken.
-std::vector<uint8_t> limited_lengths(const std::vector<uint64_t>& counts, unsigned max_bits) {
-    const size_t n_all = counts.size();
-    std::vector<uint32_t> order;
-    for (uint32_t s = 0; s < n_all; ++s) if (counts[s]) order.push_back(s);
-    std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return counts[a] < counts[b]; });
-    const size_t n = order.size();
-    std::vector<uint8_t> lengths(n_all, 0);
-    if (n == 0) return lengths;
-    if (n == 1) { lengths[order[0]] = 1; return lengths; }
-    if (n > (size_t(1) << max_bits)) fail(kInvalidCodebook, "Huff0 max_bits cannot represent every observed symbol.");
-    std::vector<uint64_t> leaf(n);
-    for (size_t i = 0; i < n; ++i) leaf[i] = counts[order[i]];
-    // is_leaf[level] flags the merged list of that level (level 0 = deepest)
-    std::vector<std::vector<uint8_t>> is_leaf(max_bits);
-    std::vector<uint64_t> below = leaf;               // weights of the previous level's list
-    is_leaf[0].assign(n, 1);
-    for (unsigned level = 1; level < max_bits; ++level) {
-        std::vector<uint64_t> merged;
-        std::vector<uint8_t>& flags = is_leaf[level];
-        size_t a = 0, b = 0;
-        const size_t packages = below.size() / 2;
-        while (a < n || b < packages) {
-            const bool take_leaf = b == packages || (a < n && leaf[a] <= below[2 * b] + below[2 * b + 1]);
-            merged.push_back(take_leaf ? leaf[a] : below[2 * b] + below[2 * b + 1]);
-            flags.push_back(take_leaf ? 1 : 0);
-            if (take_leaf) ++a; else ++b;
+// Code lengths as Zstd's HUF_buildCTable_wksp computes them (huf_compress.c
+// at the revision pinned by the reference's CMakeLists.txt:30), restated
+// from that published source:
+//   1. symbols ordered by decreasing count: each count below 166 has a
+//      bucket of its own, where symbols keep ascending order; larger counts
+//      share a bucket per power of two, ordered by Zstd's quicksort (last
+//      element as pivot, insertion sort below eight elements);
+//   2. the Huffman tree from two queues, the sorted leaves taken from their
+//      low end and the internal nodes in creation order, a leaf winning only
+//      when its count is strictly smaller;
+//   3. lengths above max_bits cut to max_bits, and the excess Kraft sum
+//      repaid by lengthening shorter codes of the least frequent symbols
+//      (HUF_setMaxHeight), then any overshoot given back.
+namespace huf {
+
+struct Node {
+    uint32_t count = 0;
+    uint16_t parent = 0;
+    uint8_t symbol = 0;
+    uint8_t bits = 0;
+};
+
+constexpr int kBuckets = 192;
+constexpr uint32_t kLogBucketsBegin = kBuckets - 1 - 32 - 1;   // 158
+constexpr uint32_t kDistinctBelow = kLogBucketsBegin + 7;       // 158 + highbit(158) = 166
+constexpr int kFirstInternal = 256;
+
+uint32_t bucket_of(uint32_t count) {
+    return count < kDistinctBelow ? count : static_cast<uint32_t>(highbit(count)) + kLogBucketsBegin;
+}
+
+void insertion_sort(Node* a, int low, int high) {
+    for (int i = low + 1; i <= high; ++i) {
+        const Node key = a[i];
+        int j = i - 1;
+        while (j >= low && a[j].count < key.count) { a[j + 1] = a[j]; --j; }
+        a[j + 1] = key;
+    }
+}
+
+int partition(Node* a, int low, int high) {
+    const uint32_t pivot = a[high].count;
+    int i = low - 1;
+    for (int j = low; j < high; ++j)
+        if (a[j].count > pivot) std::swap(a[++i], a[j]);
+    std::swap(a[i + 1], a[high]);
+    return i + 1;
+}
+
+void quick_sort(Node* a, int low, int high) {
+    if (high - low < 8) { insertion_sort(a, low, high); return; }
+    while (low < high) {
+        const int mid = partition(a, low, high);
+        if (mid - low < high - mid) { quick_sort(a, low, mid - 1); low = mid + 1; }
+        else { quick_sort(a, mid + 1, high); high = mid - 1; }
+    }
+}
+
+// Symbols 0..max_symbol by decreasing count into leaf[0..max_symbol]. The
+// symbols of bucket b are placed from first[b + 1] = the number of symbols
+// in buckets above b, in ascending symbol order.
+void sort_symbols(const uint32_t* counts, int max_symbol, Node* leaf) {
+    uint32_t first[kBuckets] = {0}, end[kBuckets] = {0};
+    for (int s = 0; s <= max_symbol; ++s) ++first[bucket_of(counts[s])];
+    for (int b = kBuckets - 1; b > 0; --b) {
+        first[b - 1] += first[b];
+        end[b - 1] = first[b - 1];
+    }
+    for (int s = 0; s <= max_symbol; ++s) {
+        Node& n = leaf[end[bucket_of(counts[s]) + 1]++];
+        n.count = counts[s];
+        n.symbol = static_cast<uint8_t>(s);
+    }
+    // only the shared buckets (from index 165, which also holds counts
+    // 166-255) can be out of order
+    for (uint32_t b = kDistinctBelow; b < kBuckets - 1; ++b) {
+        const int size = static_cast<int>(end[b] - first[b]);
+        if (size > 1) quick_sort(leaf + first[b], 0, size - 1);
+    }
+}
+
+// Returns the index of the last leaf with a nonzero count; node[i].bits is
+// each leaf's depth in the unlimited tree. node[-1] must exist (a barrier).
+int build_tree(Node* node, int max_symbol) {
+    int last = max_symbol;
+    while (node[last].count == 0) --last;
+    int low_leaf = last, low_node = kFirstInternal, next = kFirstInternal;
+    const int root = kFirstInternal + last - 1;
+    node[next].count = node[low_leaf].count + node[low_leaf - 1].count;
+    node[low_leaf].parent = node[low_leaf - 1].parent = static_cast<uint16_t>(next);
+    ++next;
+    low_leaf -= 2;
+    for (int n = next; n <= root; ++n) node[n].count = 1u << 30;
+    node[-1].count = 1u << 31;
+    auto take = [&]() { return node[low_leaf].count < node[low_node].count ? low_leaf-- : low_node++; };
+    while (next <= root) {
+        const int a = take();
+        const int b = take();
+        node[next].count = node[a].count + node[b].count;
+        node[a].parent = node[b].parent = static_cast<uint16_t>(next);
+        ++next;
+    }
+    node[root].bits = 0;
+    for (int n = root - 1; n >= kFirstInternal; --n) node[n].bits = static_cast<uint8_t>(node[node[n].parent].bits + 1);
+    for (int n = 0; n <= last; ++n) node[n].bits = static_cast<uint8_t>(node[node[n].parent].bits + 1);
+    return last;
+}
+
+// HUF_setMaxHeight: returns the table log.
+unsigned limit_height(Node* node, int last, unsigned target) {
+    const unsigned largest = node[last].bits;
+    if (largest <= target) return largest;
+    const int base_cost = 1 << (largest - target);
+    int cost = 0, n = last;
+    while (node[n].bits > target) {
+        cost += base_cost - (1 << (largest - node[n].bits));
+        node[n].bits = static_cast<uint8_t>(target);
+        --n;
+    }
+    while (node[n].bits == target) --n;
+    cost >>= (largest - target);   // a multiple of base_cost before the shift
+    constexpr uint32_t kNone = 0xF0F0F0F0u;
+    uint32_t rank_last[12 + 2];
+    std::fill(std::begin(rank_last), std::end(rank_last), kNone);
+    // rank_last[k]: the least frequent symbol whose length is target - k
+    unsigned current = target;
+    for (int pos = n; pos >= 0; --pos) {
+        if (node[pos].bits >= current) continue;
+        current = node[pos].bits;
+        rank_last[target - current] = static_cast<uint32_t>(pos);
+    }
+    while (cost > 0) {
+        unsigned dec = static_cast<unsigned>(highbit(static_cast<uint32_t>(cost))) + 1;
+        for (; dec > 1; --dec) {
+            const uint32_t high = rank_last[dec], low = rank_last[dec - 1];
+            if (high == kNone) continue;
+            if (low == kNone) break;
+            if (node[high].count <= 2 * node[low].count) break;
         }
-        below.swap(merged);
+        while (dec <= 12 && rank_last[dec] == kNone) ++dec;
+        cost -= 1 << (dec - 1);
+        ++node[rank_last[dec]].bits;
+        if (rank_last[dec - 1] == kNone) rank_last[dec - 1] = rank_last[dec];
+        if (rank_last[dec] == 0) {
+            rank_last[dec] = kNone;
+        } else {
+            --rank_last[dec];
+            if (node[rank_last[dec]].bits != target - dec) rank_last[dec] = kNone;
+        }
     }
-    std::vector<uint32_t> depth(n, 0);
-    size_t take = 2 * n - 2;
-    for (unsigned level = max_bits; level-- > 0;) {
-        size_t leaves = 0, packages = 0;
-        for (size_t i = 0; i < take; ++i) (is_leaf[level][i] ? leaves : packages) += 1;
-        for (size_t i = 0; i < leaves; ++i) ++depth[i];
-        take = 2 * packages;
+    while (cost < 0) {
+        if (rank_last[1] == kNone) {
+            while (node[n].bits == target) --n;
+            --node[n + 1].bits;
+            rank_last[1] = static_cast<uint32_t>(n + 1);
+            ++cost;
+            continue;
+        }
+        --node[rank_last[1] + 1].bits;
+        ++rank_last[1];
+        ++cost;
     }
-    for (size_t i = 0; i < n; ++i) lengths[order[i]] = static_cast<uint8_t>(depth[i]);
+    return target;
+}
+
+}  // namespace huf
+
+// Code lengths of symbols 0..255 (0 = absent) for `counts`, at most max_bits.
+std::array<uint8_t, 256> zstd_lengths(const uint32_t* counts, unsigned max_bits) {
+    int max_symbol = -1;
+    for (int s = 0; s < 256; ++s) if (counts[s]) max_symbol = s;
+    std::vector<huf::Node> storage(2 * 256 + 1);
+    huf::Node* node = storage.data() + 1;
+    huf::sort_symbols(counts, max_symbol, node);
+    const int last = huf::build_tree(node, max_symbol);
+    huf::limit_height(node, last, max_bits);
+    std::array<uint8_t, 256> lengths{};
+    for (int i = 0; i <= last; ++i) lengths[node[i].symbol] = node[i].bits;
     return lengths;
 }
 
@@ -174,79 +308,202 @@ void write_counts(LsbWriter& w, const std::vector<int>& norm, unsigned log) {
     }
 }
 
-// FSE-compresses Huffman weights with two interleaved states. For each
-// symbol, `inverse[s][y]` names the state whose successor range holds y; the
-// weights are walked backwards so every transition is a table lookup, and
-// the decoder's reads are emitted in reverse order. Empty result: FSE does
-// not apply (fewer than two distinct weights).
-std::vector<uint8_t> fse_weights(const std::vector<uint8_t>& weights) {
-    const size_t n = weights.size();
-    std::vector<uint32_t> hist(13, 0);
-    for (uint8_t w : weights) ++hist[w];
-    unsigned distinct = 0, top = 0;
-    for (unsigned s = 0; s < 13; ++s) if (hist[s]) { ++distinct; top = s; }
-    if (n < 2 || distinct < 2) return {};
-    const unsigned log = 6, size = 1u << log;
-    std::vector<int> norm(top + 1, 0);
-    int total = 0;
-    for (unsigned s = 0; s <= top; ++s) {
-        if (!hist[s]) continue;
-        norm[s] = std::max<int>(1, static_cast<int>(uint64_t(hist[s]) * size / n));
-        total += norm[s];
+// Zstd's FSE_optimalTableLog for HUF_compressWeights (at most 6 bits).
+unsigned weights_table_log(size_t n, unsigned max_symbol) {
+    const unsigned min_log = std::min<unsigned>(highbit(static_cast<uint32_t>(n)) + 1, highbit(max_symbol) + 2);
+    unsigned log = 6;
+    // unsigned, as in Zstd: below n = 5 it wraps and leaves the log at 6
+    const unsigned from_size = static_cast<unsigned>(highbit(static_cast<uint32_t>(n - 1))) - 2u;
+    if (from_size < log) log = from_size;
+    if (min_log > log) log = min_log;
+    return std::min(std::max(log, 5u), 12u);
+}
+
+// Zstd's FSE_normalizeCount with useLowProbCount = 0 (HUF_compressWeights):
+// proportional shares from one fixed-point step, small shares rounded up
+// against Zstd's thresholds, the remainder given to the largest share, or
+// the second method when that would take half of the largest.
+std::vector<int> normalize_counts(const std::vector<uint32_t>& count, uint32_t total, unsigned log) {
+    static const uint64_t kRoundUp[8] = {0, 473195, 504333, 520860, 550000, 700000, 750000, 830000};
+    const unsigned scale = 62 - log;
+    const uint64_t step = (uint64_t(1) << 62) / total;
+    const uint64_t unit = uint64_t(1) << (scale - 20);
+    const uint32_t low = total >> log;
+    std::vector<int> norm(count.size(), 0);
+    int left = 1 << log, largest = 0, largest_share = 0;
+    for (size_t s = 0; s < count.size(); ++s) {
+        if (count[s] == 0) continue;
+        if (count[s] <= low) { norm[s] = 1; --left; continue; }
+        const uint64_t scaled = uint64_t(count[s]) * step;
+        int share = static_cast<int>(scaled >> scale);
+        if (share < 8 && scaled - (uint64_t(share) << scale) > unit * kRoundUp[share]) ++share;
+        if (share > largest_share) { largest_share = share; largest = static_cast<int>(s); }
+        norm[s] = share;
+        left -= share;
     }
-    while (total != static_cast<int>(size)) {
-        const bool over = total > static_cast<int>(size);
-        int best = -1;
-        for (unsigned s = 0; s <= top; ++s)
-            if (norm[s] > (over ? 1 : 0) && (best < 0 || norm[s] > norm[best])) best = static_cast<int>(s);
-        if (best < 0) return {};
-        norm[best] += over ? -1 : 1;
-        total += over ? -1 : 1;
+    if (-left < (norm[largest] >> 1)) {
+        norm[largest] += left;
+        return norm;
     }
+    // FSE_normalizeM2
+    constexpr int kOpen = -2;
+    uint32_t rest = total, given = 0;
+    uint32_t low_one = static_cast<uint32_t>((uint64_t(total) * 3) >> (log + 1));
+    for (size_t s = 0; s < count.size(); ++s) {
+        if (count[s] == 0) { norm[s] = 0; continue; }
+        if (count[s] <= low || count[s] <= low_one) { norm[s] = 1; ++given; rest -= count[s]; continue; }
+        norm[s] = kOpen;
+    }
+    uint32_t to_give = (1u << log) - given;
+    if (to_give == 0) return norm;
+    if (rest / to_give > low_one) {
+        low_one = static_cast<uint32_t>((uint64_t(rest) * 3) / (uint64_t(to_give) * 2));
+        for (size_t s = 0; s < count.size(); ++s)
+            if (norm[s] == kOpen && count[s] <= low_one) { norm[s] = 1; ++given; rest -= count[s]; }
+        to_give = (1u << log) - given;
+    }
+    if (given == count.size()) {
+        size_t top = 0;
+        for (size_t s = 0; s < count.size(); ++s) if (count[s] > count[top]) top = s;
+        norm[top] += static_cast<int>(to_give);
+        return norm;
+    }
+    if (rest == 0) {
+        for (size_t s = 0; to_give > 0; s = (s + 1) % count.size())
+            if (norm[s] > 0) { --to_give; ++norm[s]; }
+        return norm;
+    }
+    const unsigned vlog = 62 - log;
+    const uint64_t mid = (uint64_t(1) << (vlog - 1)) - 1;
+    const uint64_t rstep = ((uint64_t(1) << vlog) * to_give + mid) / rest;
+    uint64_t acc = mid;
+    for (size_t s = 0; s < count.size(); ++s) {
+        if (norm[s] != kOpen) continue;
+        const uint64_t next = acc + count[s] * rstep;
+        const int share = static_cast<int>((next >> vlog) - (acc >> vlog));
+        if (share < 1) fail(kInvalidCodebook, "FSE normalization failed.");
+        norm[s] = share;
+        acc = next;
+    }
+    return norm;
+}
+
+// Zstd's tANS encoder with two interleaved states (FSE_buildCTable_wksp and
+// FSE_compress_usingCTable): symbols are encoded from the last to the first,
+// four per flush, into a bit container whose bytes may not reach the last
+// eight of `capacity` (an empty result then, as Zstd's overflow check).
+std::vector<uint8_t> fse_encode(const std::vector<uint8_t>& src, const std::vector<int>& norm, unsigned log,
+                                size_t capacity) {
+    const size_t n = src.size();
+    if (n <= 2 || capacity <= 8) return {};
+    const uint32_t size = 1u << log;
     const auto table = spread(norm, log);
-    std::vector<std::vector<int>> inverse(top + 1, std::vector<int>(size, -1));
-    std::vector<int> deep(top + 1, -1);   // a state with at least one bit to read
-    for (unsigned u = 0; u < size; ++u) {
-        const Cell& c = table[u];
-        for (unsigned y = c.base; y < c.base + (1u << c.bits); ++y) inverse[c.symbol][y] = static_cast<int>(u);
-        if (c.bits && deep[c.symbol] < 0) deep[c.symbol] = static_cast<int>(u);
-    }
-    // state sequences: stream j decodes weights j, j + 2, ...
-    const size_t per[2] = {(n + 1) / 2, n / 2};
-    const int over_stream = static_cast<int>((n - 2) & 1);
-    std::vector<int> state[2] = {std::vector<int>(per[0]), std::vector<int>(per[1])};
-    for (int j = 0; j < 2; ++j) {
-        const size_t last = per[j] - 1;
-        const uint8_t sym = weights[2 * last + j];
-        int pick = j == over_stream ? deep[sym] : -1;
-        if (pick < 0) for (unsigned u = 0; u < size && pick < 0; ++u) if (table[u].symbol == sym) pick = static_cast<int>(u);
-        if (pick < 0) return {};
-        state[j][last] = pick;
-        for (size_t k = last; k-- > 0;) {
-            const int u = inverse[weights[2 * k + j]][state[j][k + 1]];
-            if (u < 0) fail(kInvalidCodebook, "FSE weight encoder found no state.");
-            state[j][k] = u;
+    std::vector<uint32_t> cumul(norm.size() + 1, 0);
+    for (size_t s = 0; s < norm.size(); ++s) cumul[s + 1] = cumul[s] + static_cast<uint32_t>(norm[s] < 0 ? 1 : norm[s]);
+    std::vector<uint16_t> next_state(size);
+    for (uint32_t u = 0; u < size; ++u) next_state[cumul[table[u].symbol]++] = static_cast<uint16_t>(size + u);
+    std::vector<uint32_t> delta_bits(norm.size());
+    std::vector<int32_t> delta_state(norm.size());
+    int32_t total = 0;
+    for (size_t s = 0; s < norm.size(); ++s) {
+        const int c = norm[s];
+        if (c == 0) {
+            delta_bits[s] = ((log + 1) << 16) - size;
+        } else if (c == 1 || c == -1) {
+            delta_bits[s] = (log << 16) - size;
+            delta_state[s] = total - 1;
+            total += 1;
+        } else {
+            const uint32_t out_bits = log - static_cast<uint32_t>(highbit(static_cast<uint32_t>(c - 1)));
+            delta_bits[s] = (out_bits << 16) - (static_cast<uint32_t>(c) << out_bits);
+            delta_state[s] = total - c;
+            total += c;
         }
     }
-    struct Read { uint32_t value; unsigned bits; };
-    std::vector<Read> reads;
-    reads.push_back({static_cast<uint32_t>(state[0][0]), log});
-    reads.push_back({static_cast<uint32_t>(state[1][0]), log});
-    for (size_t i = 0; i < n; ++i) {
-        const int j = static_cast<int>(i & 1);
-        const size_t k = i >> 1;
-        if (k + 1 >= per[j]) continue;
-        const Cell& c = table[state[j][k]];
-        reads.push_back({static_cast<uint32_t>(state[j][k + 1] - c.base), c.bits});
+    std::vector<uint8_t> out;
+    const size_t limit = capacity - 8;
+    uint64_t bits = 0;
+    unsigned fill = 0;
+    auto add = [&](uint32_t value, unsigned nb) {
+        bits |= (uint64_t(value) & ((uint64_t(1) << nb) - 1)) << fill;
+        fill += nb;
+    };
+    auto flush = [&]() {
+        for (unsigned k = 0; k < fill / 8; ++k) out.push_back(static_cast<uint8_t>(bits >> (8 * k)));
+        bits = fill >= 64 ? 0 : bits >> (fill / 8 * 8);
+        fill &= 7;
+        if (out.size() > limit) out.resize(limit);
+    };
+    auto start = [&](uint8_t s) {
+        const uint32_t nb = (delta_bits[s] + (1u << 15)) >> 16;
+        const uint32_t v = (nb << 16) - delta_bits[s];
+        return static_cast<uint32_t>(next_state[(v >> nb) + delta_state[s]]);
+    };
+    auto encode = [&](uint32_t& state, uint8_t s) {
+        const uint32_t nb = (state + delta_bits[s]) >> 16;
+        add(state, nb);
+        state = next_state[(state >> nb) + delta_state[s]];
+    };
+    size_t i = n;
+    uint32_t one, two;
+    if (n & 1) {
+        one = start(src[--i]);
+        two = start(src[--i]);
+        encode(one, src[--i]);
+        flush();
+    } else {
+        two = start(src[--i]);
+        one = start(src[--i]);
     }
+    if ((n - 2) & 2) {
+        encode(two, src[--i]);
+        encode(one, src[--i]);
+        flush();
+    }
+    while (i > 0) {
+        encode(two, src[--i]);
+        encode(one, src[--i]);
+        encode(two, src[--i]);
+        encode(one, src[--i]);
+        flush();
+    }
+    add(two, log);
+    flush();
+    add(one, log);
+    flush();
+    add(1, 1);   // end mark
+    flush();
+    if (out.size() >= limit) return {};
+    if (fill) out.push_back(static_cast<uint8_t>(bits));
+    return out;
+}
+
+// HUF_compressWeights: the weights' FSE table description and stream in at
+// most `capacity` bytes. Returns one byte for a single repeated weight and
+// nothing when FSE does not apply (Zstd's 1 and 0).
+std::vector<uint8_t> compress_weights(const std::vector<uint8_t>& weights, size_t capacity) {
+    const size_t n = weights.size();
+    if (n <= 1) return {};
+    std::vector<uint32_t> hist(13, 0);
+    for (uint8_t w : weights) ++hist[w];
+    unsigned top = 0;
+    uint32_t most = 0;
+    for (unsigned s = 0; s < 13; ++s) {
+        if (hist[s]) top = s;
+        most = std::max(most, hist[s]);
+    }
+    if (most == n) return {0};
+    if (most == 1) return {};
+    hist.resize(top + 1);
+    const unsigned log = weights_table_log(n, top);
+    const auto norm = normalize_counts(hist, static_cast<uint32_t>(n), log);
     std::vector<uint8_t> out;
     LsbWriter head(out);
     write_counts(head, norm, log);
     head.close(false);
-    std::vector<uint8_t> body;
-    LsbWriter w(body);
-    for (size_t r = reads.size(); r-- > 0;) w.put(reads[r].value, reads[r].bits);
-    w.close(true);
+    if (out.size() >= capacity) return {};
+    const auto body = fse_encode(weights, norm, log, capacity - out.size());
+    if (body.empty()) return {};
     out.insert(out.end(), body.begin(), body.end());
     return out;
 }
@@ -255,15 +512,19 @@ std::vector<uint8_t> fse_weights(const std::vector<uint8_t>& weights) {
 
 // ------------------------------------------------------------------ Huff0
 std::vector<uint8_t> huff0_header_from_lengths(const std::array<uint8_t, 256>& lengths) {
+    // HUF_writeCTable_wksp into the reference's HUF_CTABLEBOUND (129) bytes
+    // (codebooks.h:27-36): FSE-compressed weights when they take more than
+    // one byte and fewer than last / 2, else 4-bit weights, which hold at
+    // most 128 symbols
     unsigned log = 0, last = 0, present = 0;
     for (unsigned s = 0; s < 256; ++s)
         if (lengths[s]) { log = std::max<unsigned>(log, lengths[s]); last = s; ++present; }
     if (present < 2) fail(kInvalidCodebook, "Huff0 requires at least two symbols.");
     std::vector<uint8_t> weights(last);
     for (unsigned s = 0; s < last; ++s) weights[s] = lengths[s] ? static_cast<uint8_t>(log + 1 - lengths[s]) : 0;
-    const auto fse = fse_weights(weights);
+    const auto fse = compress_weights(weights, 128);
     std::vector<uint8_t> header;
-    if (!fse.empty() && fse.size() < 128 && (last > 128 || fse.size() < (last + 1) / 2)) {
+    if (fse.size() > 1 && fse.size() < last / 2) {
         header.push_back(static_cast<uint8_t>(fse.size()));
         header.insert(header.end(), fse.begin(), fse.end());
         return header;
@@ -297,18 +558,15 @@ std::vector<uint8_t> huff0_build(const uint64_t* counts, uint32_t prior, unsigne
         }
         if (shift == 64) fail(kLayoutLimit, "Huff0 symbol count overflow.");
     }
-    std::vector<uint64_t> scaled(256);
+    uint32_t scaled[256];
     unsigned present = 0;
     for (int s = 0; s < 256; ++s) {
-        scaled[s] = (counts[s] ? std::max<uint64_t>(1, counts[s] >> shift) : 0) + prior;
+        scaled[s] = static_cast<uint32_t>((counts[s] ? std::max<uint64_t>(1, counts[s] >> shift) : 0) + prior);
         present += scaled[s] > 0;
     }
     if (present < 2) fail(kInvalidCodebook, "Huff0 requires at least two symbols.");
     if (present > (1u << max_bits)) fail(kInvalidCodebook, "Huff0 max_bits cannot represent every observed symbol.");
-    const auto lengths = limited_lengths(scaled, max_bits);
-    std::array<uint8_t, 256> table{};
-    std::copy(lengths.begin(), lengths.end(), table.begin());
-    return huff0_header_from_lengths(table);
+    return huff0_header_from_lengths(zstd_lengths(scaled, max_bits));
 }
 
 Huff0Tables huff0_tables(const std::array<uint8_t, 256>& lengths) {

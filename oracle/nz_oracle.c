@@ -653,71 +653,158 @@ nzo_huf* nzo_huf_from_header(const uint8_t* src, size_t size, size_t* consumed) 
     return h;
 }
 
-/* --- code construction: boundary package-merge (optimal lengths <= L) --- */
-typedef struct { uint64_t weight; int leaf; int left, right; } pm_node;
+/* --- code construction: Zstd's HUF_buildCTable_wksp ---------------------
+ * codebooks.h:1-42 hands the scaled histogram to Zstd's HUF_buildCTable_wksp
+ * (huf_compress.c at the revision pinned by CMakeLists.txt:30; Zstd is not
+ * vendored in the reference). Restated from that published source: symbols
+ * sorted by decreasing count (HUF_sort), the two-queue Huffman tree
+ * (HUF_buildTree), then the height limit (HUF_setMaxHeight). Pinned against
+ * the tree descriptions libzstd itself writes (tests/golden/huff0_tables.json). */
+typedef struct { uint32_t count; int parent; int symbol; int bits; } huf_node;
 
-static int cmp_leaf(const void* a, const void* b, void* ctx) {
-    const uint32_t* counts = ctx;
-    const int x = *(const int*)a, y = *(const int*)b;
-    if (counts[x] != counts[y]) return counts[x] < counts[y] ? -1 : 1;
-    return x - y;
+#define HUF_BUCKETS 192
+#define HUF_LOG_BUCKETS_BEGIN 158   /* HUF_BUCKETS - 1 - 32 - 1 */
+#define HUF_DISTINCT_CUTOFF 166     /* 158 + highbit(158) */
+
+static int huf_bucket(uint32_t c) {
+    return c < HUF_DISTINCT_CUTOFF ? (int)c : highbit32(c) + HUF_LOG_BUCKETS_BEGIN;
 }
 
-static void sort_leaves(int* idx, int n, const uint32_t* counts) {
-    for (int i = 1; i < n; ++i) {   /* insertion sort, n <= 256 */
-        int v = idx[i], j = i - 1;
-        while (j >= 0 && cmp_leaf(&idx[j], &v, (void*)counts) > 0) { idx[j + 1] = idx[j]; --j; }
-        idx[j + 1] = v;
+static void huf_insertion(huf_node* a, int lo, int hi) {
+    for (int i = lo + 1; i <= hi; ++i) {
+        huf_node key = a[i];
+        int j = i - 1;
+        while (j >= lo && a[j].count < key.count) { a[j + 1] = a[j]; --j; }
+        a[j + 1] = key;
     }
 }
 
-static void pm_count(const pm_node* nodes, int id, uint8_t* lengths) {
-    if (nodes[id].leaf >= 0) { ++lengths[nodes[id].leaf]; return; }
-    pm_count(nodes, nodes[id].left, lengths);
-    pm_count(nodes, nodes[id].right, lengths);
+static void huf_swap(huf_node* a, huf_node* b) { huf_node t = *a; *a = *b; *b = t; }
+
+static void huf_quick(huf_node* a, int lo, int hi) {
+    if (hi - lo < 8) { huf_insertion(a, lo, hi); return; }
+    while (lo < hi) {
+        const uint32_t pivot = a[hi].count;   /* last element */
+        int i = lo - 1;
+        for (int j = lo; j < hi; ++j) if (a[j].count > pivot) huf_swap(&a[++i], &a[j]);
+        huf_swap(&a[i + 1], &a[hi]);
+        const int mid = i + 1;
+        if (mid - lo < hi - mid) { huf_quick(a, lo, mid - 1); lo = mid + 1; }
+        else { huf_quick(a, mid + 1, hi); hi = mid - 1; }
+    }
+}
+
+/* node[-1] must be addressable: the tree build uses it as a barrier. */
+static int huf_zstd_tree(const uint32_t* counts, int max_symbol, huf_node* node) {
+    /* HUF_sort: bucket b's symbols start after every symbol of buckets > b */
+    int base[HUF_BUCKETS] = {0}, curr[HUF_BUCKETS] = {0};
+    for (int s = 0; s <= max_symbol; ++s) ++base[huf_bucket(counts[s])];
+    for (int b = HUF_BUCKETS - 1; b > 0; --b) { base[b - 1] += base[b]; curr[b - 1] = base[b - 1]; }
+    for (int s = 0; s <= max_symbol; ++s) {
+        const int pos = curr[huf_bucket(counts[s]) + 1]++;
+        node[pos].count = counts[s];
+        node[pos].symbol = s;
+    }
+    for (int b = HUF_DISTINCT_CUTOFF; b < HUF_BUCKETS - 1; ++b)
+        if (curr[b] - base[b] > 1) huf_quick(node + base[b], 0, curr[b] - base[b] - 1);
+    /* HUF_buildTree */
+    int last = max_symbol;
+    while (node[last].count == 0) --last;
+    const int first_internal = 256, root = first_internal + last - 1;
+    int ls = last, ln = first_internal, nb = first_internal;
+    node[nb].count = node[ls].count + node[ls - 1].count;
+    node[ls].parent = node[ls - 1].parent = nb;
+    ++nb;
+    ls -= 2;
+    for (int n = nb; n <= root; ++n) node[n].count = 1u << 30;
+    node[-1].count = 1u << 31;
+    while (nb <= root) {
+        const int a = node[ls].count < node[ln].count ? ls-- : ln++;
+        const int b = node[ls].count < node[ln].count ? ls-- : ln++;
+        node[nb].count = node[a].count + node[b].count;
+        node[a].parent = node[b].parent = nb;
+        ++nb;
+    }
+    node[root].bits = 0;
+    for (int n = root - 1; n >= first_internal; --n) node[n].bits = node[node[n].parent].bits + 1;
+    for (int n = 0; n <= last; ++n) node[n].bits = node[node[n].parent].bits + 1;
+    return last;
+}
+
+/* HUF_setMaxHeight on the sorted leaves node[0..last]. */
+static void huf_zstd_limit(huf_node* node, int last, int target) {
+    const int largest = node[last].bits;
+    if (largest <= target) return;
+    const int base_cost = 1 << (largest - target);
+    int total = 0, n = last;
+    while (node[n].bits > target) {
+        total += base_cost - (1 << (largest - node[n].bits));
+        node[n].bits = target;
+        --n;
+    }
+    while (node[n].bits == target) --n;
+    total >>= largest - target;
+    const uint32_t none = 0xF0F0F0F0u;
+    uint32_t rank_last[HUF_MAX_BITS + 2];
+    for (int k = 0; k < HUF_MAX_BITS + 2; ++k) rank_last[k] = none;
+    int current = target;
+    for (int pos = n; pos >= 0; --pos) {
+        if (node[pos].bits >= current) continue;
+        current = node[pos].bits;
+        rank_last[target - current] = (uint32_t)pos;
+    }
+    while (total > 0) {
+        int k = highbit32((uint32_t)total) + 1;
+        for (; k > 1; --k) {
+            const uint32_t hi = rank_last[k], lo = rank_last[k - 1];
+            if (hi == none) continue;
+            if (lo == none) break;
+            if (node[hi].count <= 2 * node[lo].count) break;
+        }
+        while (k <= HUF_MAX_BITS && rank_last[k] == none) ++k;
+        total -= 1 << (k - 1);
+        node[rank_last[k]].bits++;
+        if (rank_last[k - 1] == none) rank_last[k - 1] = rank_last[k];
+        if (rank_last[k] == 0) {
+            rank_last[k] = none;
+        } else {
+            rank_last[k]--;
+            if (node[rank_last[k]].bits != target - k) rank_last[k] = none;
+        }
+    }
+    while (total < 0) {
+        if (rank_last[1] == none) {
+            while (node[n].bits == target) --n;
+            node[n + 1].bits--;
+            rank_last[1] = (uint32_t)(n + 1);
+            ++total;
+            continue;
+        }
+        node[rank_last[1] + 1].bits--;
+        rank_last[1]++;
+        ++total;
+    }
 }
 
 nzo_huf* nzo_huf_from_counts(const uint32_t* counts, int max_bits) {
-    int leaves[256], n = 0;
-    for (int s = 0; s < 256; ++s) if (counts[s]) leaves[n++] = s;
-    if (n < 2) { fail("Huff0 requires at least two symbols."); return NULL; }
-    if (max_bits < 1 || max_bits > HUF_MAX_BITS || n > (1 << max_bits)) {
+    int present = 0, max_symbol = 0;
+    uint64_t total = 0;
+    for (int s = 0; s < 256; ++s) if (counts[s]) { ++present; max_symbol = s; total += counts[s]; }
+    /* the tree's unbuilt nodes read as 2^30: the reference scales histograms
+     * below that first (binding_helpers.h:33-57) */
+    if (total >= (1u << 30)) { fail("Huff0 symbol count overflow."); return NULL; }
+    if (present < 2) { fail("Huff0 requires at least two symbols."); return NULL; }
+    if (max_bits < 1 || max_bits > HUF_MAX_BITS || present > (1 << max_bits)) {
         fail("Huff0 max_bits cannot represent every observed symbol.");
         return NULL;
     }
-    sort_leaves(leaves, n, counts);
-    const int cap = 2 * n * (max_bits + 1) + 8;
-    pm_node* nodes = malloc(sizeof(pm_node) * cap);
-    int* prev = malloc(sizeof(int) * 2 * n);
-    int* cur = malloc(sizeof(int) * 2 * n);
-    int* packs = malloc(sizeof(int) * n);
-    int used = 0, prev_n = 0;
-    int leaf_ids[256];
-    for (int i = 0; i < n; ++i) {
-        nodes[used] = (pm_node){counts[leaves[i]], leaves[i], -1, -1};
-        leaf_ids[i] = used;
-        prev[prev_n++] = used++;
-    }
-    for (int level = 1; level < max_bits; ++level) {
-        int n_packs = 0;
-        for (int k = 0; k + 1 < prev_n; k += 2) {
-            nodes[used] = (pm_node){nodes[prev[k]].weight + nodes[prev[k + 1]].weight, -1,
-                                    prev[k], prev[k + 1]};
-            packs[n_packs++] = used++;
-        }
-        int a = 0, b = 0, m = 0;
-        while (a < n || b < n_packs) {
-            if (b == n_packs || (a < n && nodes[leaf_ids[a]].weight <= nodes[packs[b]].weight))
-                cur[m++] = leaf_ids[a++];
-            else
-                cur[m++] = packs[b++];
-        }
-        int* t = prev; prev = cur; cur = t;
-        prev_n = m;
-    }
+    huf_node storage[2 * 256 + 1];
+    memset(storage, 0, sizeof storage);
+    huf_node* node = storage + 1;
+    const int last = huf_zstd_tree(counts, max_symbol, node);
+    huf_zstd_limit(node, last, max_bits);
     uint8_t lengths[256] = {0};
-    for (int i = 0; i < 2 * n - 2; ++i) pm_count(nodes, prev[i], lengths);
-    free(nodes); free(prev); free(cur); free(packs);
+    for (int i = 0; i <= last; ++i) lengths[node[i].symbol] = (uint8_t)node[i].bits;
     return nzo_huf_from_lengths(lengths);
 }
 
@@ -801,101 +888,221 @@ static void fse_write_ncount(fwd_writer* w, const int16_t* norm, int max_symbol,
     }
 }
 
-/* FSE-compress the weights by inverting the decoder: walk the weights from
- * the end, pick for each symbol the state whose next-state range holds the
- * already chosen successor, and record the bits that the decoder will read. */
-static int64_t fse_encode_weights(const uint8_t* weights, int n, uint8_t* out, size_t cap) {
-    if (n < 2) return 0;
-    uint32_t hist[16] = {0};
-    int max_symbol = 0, distinct = 0;
-    for (int i = 0; i < n; ++i) { ++hist[weights[i]]; if (weights[i] > max_symbol) max_symbol = weights[i]; }
-    for (int s = 0; s <= max_symbol; ++s) distinct += hist[s] > 0;
-    if (distinct < 2) return 0;
-    const int log = 6, size = 1 << log;
-    int16_t norm[16] = {0};
+/* --- tree description: Zstd's HUF_writeCTable_wksp ----------------------
+ * The weights go through HUF_compressWeights (huf_compress.c): Zstd's
+ * FSE_optimalTableLog (at most 6), FSE_normalizeCount with useLowProbCount 0
+ * (and FSE_normalizeM2 when the remainder is too large), FSE_writeNCount,
+ * and FSE_compress_usingCTable with two interleaved states and Zstd's bit
+ * container, whose overflow check makes the weights "not compressible" when
+ * the stream reaches the last 8 bytes of the buffer. */
+static int fse_zstd_log(int n, int max_symbol) {
+    const unsigned from_size = (unsigned)highbit32((uint32_t)(n - 1)) - 2u;   /* wraps for n < 5 */
+    const int min_src = highbit32((uint32_t)n) + 1, min_sym = highbit32((uint32_t)max_symbol) + 2;
+    const int min_log = min_src < min_sym ? min_src : min_sym;
+    int log = 6;
+    if (from_size < (unsigned)log) log = (int)from_size;
+    if (min_log > log) log = min_log;
+    if (log < 5) log = 5;
+    if (log > 12) log = 12;
+    return log;
+}
+
+static int fse_zstd_normalize(int16_t* norm, int log, const uint32_t* count, uint32_t total, int max_symbol) {
+    static const uint64_t rtb[8] = {0, 473195, 504333, 520860, 550000, 700000, 750000, 830000};
+    const int scale = 62 - log;
+    const uint64_t step = ((uint64_t)1 << 62) / total;
+    const uint64_t vstep = (uint64_t)1 << (scale - 20);
+    const uint32_t low_threshold = total >> log;
+    int still = 1 << log, largest = 0, largest_p = 0;
+    for (int s = 0; s <= max_symbol; ++s) {
+        norm[s] = 0;
+        if (count[s] == 0) continue;
+        if (count[s] <= low_threshold) { norm[s] = 1; --still; continue; }
+        int p = (int)((count[s] * step) >> scale);
+        if (p < 8) p += (count[s] * step) - ((uint64_t)p << scale) > vstep * rtb[p];
+        if (p > largest_p) { largest_p = p; largest = s; }
+        norm[s] = (int16_t)p;
+        still -= p;
+    }
+    if (-still < (norm[largest] >> 1)) { norm[largest] = (int16_t)(norm[largest] + still); return 0; }
+    /* FSE_normalizeM2 */
+    const int16_t open = -2;
+    uint32_t distributed = 0, rest = total;
+    uint32_t low_one = (uint32_t)(((uint64_t)total * 3) >> (log + 1));
+    for (int s = 0; s <= max_symbol; ++s) {
+        if (count[s] == 0) { norm[s] = 0; continue; }
+        if (count[s] <= low_threshold || count[s] <= low_one) { norm[s] = 1; ++distributed; rest -= count[s]; continue; }
+        norm[s] = open;
+    }
+    uint32_t to_distribute = (1u << log) - distributed;
+    if (to_distribute == 0) return 0;
+    if (rest / to_distribute > low_one) {
+        low_one = (uint32_t)(((uint64_t)rest * 3) / ((uint64_t)to_distribute * 2));
+        for (int s = 0; s <= max_symbol; ++s)
+            if (norm[s] == open && count[s] <= low_one) { norm[s] = 1; ++distributed; rest -= count[s]; }
+        to_distribute = (1u << log) - distributed;
+    }
+    if (distributed == (uint32_t)max_symbol + 1) {
+        int max_v = 0;
+        uint32_t max_c = 0;
+        for (int s = 0; s <= max_symbol; ++s) if (count[s] > max_c) { max_v = s; max_c = count[s]; }
+        norm[max_v] = (int16_t)(norm[max_v] + (int)to_distribute);
+        return 0;
+    }
+    if (rest == 0) {
+        for (int s = 0; to_distribute > 0; s = (s + 1) % (max_symbol + 1))
+            if (norm[s] > 0) { --to_distribute; ++norm[s]; }
+        return 0;
+    }
+    const int vlog = 62 - log;
+    const uint64_t mid = ((uint64_t)1 << (vlog - 1)) - 1;
+    const uint64_t rstep = ((((uint64_t)1 << vlog) * to_distribute) + mid) / rest;
+    uint64_t acc = mid;
+    for (int s = 0; s <= max_symbol; ++s) {
+        if (norm[s] != open) continue;
+        const uint64_t end = acc + count[s] * rstep;
+        const int w = (int)((end >> vlog) - (acc >> vlog));
+        if (w < 1) return fail("FSE normalization failed.");
+        norm[s] = (int16_t)w;
+        acc = end;
+    }
+    return 0;
+}
+
+/* Zstd's BIT_CStream_t: a 64-bit container flushed in whole bytes; the write
+ * position stops 8 bytes before the end of the buffer, and closing fails
+ * (returns 0) once it has reached that point. */
+typedef struct { uint8_t* start; size_t pos, limit; uint64_t container; int bits; } zbit;
+
+static void zbit_add(zbit* b, uint64_t value, int n) {
+    b->container |= (value & (((uint64_t)1 << n) - 1)) << b->bits;
+    b->bits += n;
+}
+
+static void zbit_flush(zbit* b) {
+    const int bytes = b->bits >> 3;
+    for (int k = 0; k < bytes; ++k)
+        if (b->pos + (size_t)k < b->limit + 8) b->start[b->pos + (size_t)k] = (uint8_t)(b->container >> (8 * k));
+    b->pos += (size_t)bytes;
+    if (b->pos > b->limit) b->pos = b->limit;
+    b->bits &= 7;
+    b->container = bytes == 8 ? 0 : b->container >> (8 * bytes);
+}
+
+static size_t zbit_close(zbit* b) {
+    zbit_add(b, 1, 1);
+    zbit_flush(b);
+    if (b->pos >= b->limit) return 0;
+    if (b->bits) b->start[b->pos] = (uint8_t)b->container;
+    return b->pos + (b->bits > 0);
+}
+
+typedef struct { uint16_t next_state[64]; uint32_t delta_bits[16]; int delta_state[16]; } fse_ctable;
+
+static uint32_t fse_zstd_init_state(const fse_ctable* t, uint8_t sym) {
+    const uint32_t nb = (t->delta_bits[sym] + (1u << 15)) >> 16;
+    const uint32_t v = (nb << 16) - t->delta_bits[sym];
+    return t->next_state[(int)(v >> nb) + t->delta_state[sym]];
+}
+
+static void fse_zstd_encode(const fse_ctable* t, zbit* b, uint32_t* state, uint8_t sym) {
+    const uint32_t nb = (*state + t->delta_bits[sym]) >> 16;
+    zbit_add(b, *state, (int)nb);
+    *state = t->next_state[(int)(*state >> nb) + t->delta_state[sym]];
+}
+
+static size_t fse_zstd_compress(const uint8_t* src, int n, const int16_t* norm, int max_symbol, int log,
+                                uint8_t* dst, size_t cap) {
+    if (n <= 2 || cap <= 8) return 0;
+    const int size = 1 << log;
+    fse_cell table[64];
+    if (fse_build(norm, max_symbol, log, table, NULL) < 0) return 0;
+    /* FSE_buildCTable_wksp: next states by symbol, and per-symbol transforms */
+    fse_ctable t;
+    int cumul[17] = {0};
+    for (int s = 0; s <= max_symbol; ++s) cumul[s + 1] = cumul[s] + (norm[s] < 0 ? 1 : norm[s]);
+    for (int u = 0; u < size; ++u) t.next_state[cumul[table[u].symbol]++] = (uint16_t)(size + u);
     int total = 0;
     for (int s = 0; s <= max_symbol; ++s) {
-        if (!hist[s]) continue;
-        int v = (int)((uint64_t)hist[s] * size / (uint32_t)n);
-        if (v < 1) v = 1;
-        norm[s] = (int16_t)v;
-        total += v;
-    }
-    while (total != size) {   /* move the difference onto the largest counts */
-        int best = -1;
-        for (int s = 0; s <= max_symbol; ++s)
-            if (norm[s] > (total > size ? 1 : 0) && (best < 0 || norm[s] > norm[best])) best = s;
-        if (best < 0) return 0;
-        norm[best] = (int16_t)(norm[best] + (total > size ? -1 : 1));
-        total += total > size ? -1 : 1;
-    }
-    fse_cell table[64];
-    if (fse_build(norm, max_symbol, log, table, NULL) < 0) return -1;
-    /* decoder read order: S1, S2 (log bits each), then alternating updates */
-    uint32_t reads_v[600];
-    int reads_n[600], n_reads = 0;
-    /* choose states backward; state index k of stream j decodes weight 2k+j */
-    int st[2][256];
-    const int per[2] = {(n + 1) / 2, n / 2};
-    /* which stream's final update overflows: the stream that emits weight n-2 */
-    const int over = (n - 2) & 1;
-    for (int j = 0; j < 2; ++j) {
-        const int last = per[j] - 1;
-        const uint8_t sym = weights[2 * last + j];
-        int chosen = -1;
-        for (int u = 0; u < size; ++u) {
-            if (table[u].symbol != sym) continue;
-            if (j == over && table[u].nb_bits == 0) continue;
-            chosen = u;
-            break;
-        }
-        if (chosen < 0) return 0;
-        st[j][last] = chosen;
-        for (int k = last - 1; k >= 0; --k) {
-            const uint8_t s = weights[2 * k + j];
-            const int succ = st[j][k + 1];
-            int found = -1;
-            for (int u = 0; u < size; ++u) {
-                if (table[u].symbol != s) continue;
-                if (succ >= table[u].base && succ < table[u].base + (1 << table[u].nb_bits)) { found = u; break; }
-            }
-            if (found < 0) return fail("FSE weight encoder found no state.");
-            st[j][k] = found;
+        t.delta_state[s] = 0;
+        if (norm[s] == 0) {
+            t.delta_bits[s] = (uint32_t)(((log + 1) << 16) - size);
+        } else if (norm[s] == 1 || norm[s] == -1) {
+            t.delta_bits[s] = (uint32_t)((log << 16) - size);
+            t.delta_state[s] = total - 1;
+            total += 1;
+        } else {
+            const int out_bits = log - highbit32((uint32_t)(norm[s] - 1));
+            t.delta_bits[s] = (uint32_t)((out_bits << 16) - (norm[s] << out_bits));
+            t.delta_state[s] = total - norm[s];
+            total += norm[s];
         }
     }
-    reads_v[n_reads] = (uint32_t)st[0][0]; reads_n[n_reads++] = log;
-    reads_v[n_reads] = (uint32_t)st[1][0]; reads_n[n_reads++] = log;
-    /* updates in decode order, excluding the final overflowing one */
-    for (int i = 0; i < n; ++i) {
-        const int j = i & 1, k = i >> 1;
-        if (k + 1 >= per[j]) continue;            /* no successor: final symbol */
-        const int u = st[j][k], succ = st[j][k + 1];
-        reads_v[n_reads] = (uint32_t)(succ - table[u].base);
-        reads_n[n_reads++] = table[u].nb_bits;
+    zbit b = {dst, 0, cap - 8, 0, 0};
+    int i = n;
+    uint32_t s1, s2;
+    if (n & 1) {
+        s1 = fse_zstd_init_state(&t, src[--i]);
+        s2 = fse_zstd_init_state(&t, src[--i]);
+        fse_zstd_encode(&t, &b, &s1, src[--i]);
+        zbit_flush(&b);
+    } else {
+        s2 = fse_zstd_init_state(&t, src[--i]);
+        s1 = fse_zstd_init_state(&t, src[--i]);
     }
+    if ((n - 2) & 2) {
+        fse_zstd_encode(&t, &b, &s2, src[--i]);
+        fse_zstd_encode(&t, &b, &s1, src[--i]);
+        zbit_flush(&b);
+    }
+    while (i > 0) {
+        fse_zstd_encode(&t, &b, &s2, src[--i]);
+        fse_zstd_encode(&t, &b, &s1, src[--i]);
+        fse_zstd_encode(&t, &b, &s2, src[--i]);
+        fse_zstd_encode(&t, &b, &s1, src[--i]);
+        zbit_flush(&b);
+    }
+    zbit_add(&b, s2, log);
+    zbit_flush(&b);
+    zbit_add(&b, s1, log);
+    zbit_flush(&b);
+    return zbit_close(&b);
+}
+
+/* HUF_compressWeights: returns the bytes written, 1 for a single repeated
+ * weight, 0 when FSE does not apply. */
+static int64_t fse_encode_weights(const uint8_t* weights, int n, uint8_t* out, size_t cap) {
+    if (n <= 1) return 0;
+    uint32_t hist[16] = {0};
+    int max_symbol = 0;
+    uint32_t most = 0;
+    for (int i = 0; i < n; ++i) { ++hist[weights[i]]; if (weights[i] > max_symbol) max_symbol = weights[i]; }
+    for (int s = 0; s <= max_symbol; ++s) if (hist[s] > most) most = hist[s];
+    if (most == (uint32_t)n) return 1;
+    if (most == 1) return 0;
+    const int log = fse_zstd_log(n, max_symbol);
+    int16_t norm[16] = {0};
+    if (fse_zstd_normalize(norm, log, hist, (uint32_t)n, max_symbol) < 0) return -1;
     fwd_writer w = {out, cap, 0, 0, 0, 0};
     fse_write_ncount(&w, norm, max_symbol, log);
     fwd_close(&w, 0);
-    const size_t header = w.pos;
     if (w.overflow) return 0;
-    fwd_writer b = {out + header, cap - header, 0, 0, 0, 0};
-    for (int r = n_reads - 1; r >= 0; --r) {
-        /* each read takes its value most significant bit first from the top */
-        fwd_put(&b, reads_v[r], reads_n[r]);
-    }
-    const size_t body = fwd_close(&b, 1);
-    if (!body) return 0;
-    return (int64_t)(header + body);
+    const size_t body = fse_zstd_compress(weights, n, norm, max_symbol, log, out + w.pos, cap - w.pos);
+    if (body == 0) return 0;
+    return (int64_t)(w.pos + body);
 }
 
 int64_t nzo_huf_write_header(const nzo_huf* h, uint8_t* out, size_t cap) {
+    /* HUF_writeCTable_wksp into the reference's HUF_CTABLEBOUND (129) bytes
+     * (codebooks.h:27-36): FSE weights if they take more than one byte and
+     * fewer than max_symbol / 2, else 4-bit weights (at most 128 of them). */
     const int n = h->max_symbol;   /* weights stored for symbols 0..n-1 */
     uint8_t weights[256];
     for (int s = 0; s < n; ++s) weights[s] = h->weight[s];
-    uint8_t tmp[256];
+    uint8_t tmp[128];
     const int64_t fse = fse_encode_weights(weights, n, tmp, sizeof tmp);
     if (fse < 0) return -1;
-    if (fse > 0 && fse < 128 && (n > 128 || fse < (n + 1) / 2)) {
+    if (fse > 1 && fse < n / 2) {
         if ((size_t)fse + 1 > cap) return 0;
         out[0] = (uint8_t)fse;
         memcpy(out + 1, tmp, (size_t)fse);

@@ -67,6 +67,52 @@ def literal_blocks(frame):
         raise ValueError("trailing bytes after the frame")
 
 
+def huffman_literal_sections(frame):
+    """Yield the Huffman literals section of every compressed block of one
+    frame that carries its own tree description, whether or not the block
+    also has sequences: dicts with `tree`, `payload`, `streams` and
+    `regenerated` (the literals' count, not the block's content size)."""
+    if frame[:4] != MAGIC:
+        raise ValueError("not a zstd frame")
+    descriptor = frame[4]
+    fcs_flag, single = descriptor >> 6, (descriptor >> 5) & 1
+    dict_flag = descriptor & 3
+    pos = 5 + (0 if single else 1) + (0, 1, 2, 4)[dict_flag]
+    pos += (1 if single else 0, 2, 4, 8)[fcs_flag]
+    while True:
+        header = int.from_bytes(frame[pos:pos + 3], "little")
+        pos += 3
+        last, kind, size = header & 1, (header >> 1) & 3, header >> 3
+        if kind == 1:
+            pos += 1
+        else:
+            if kind == 2 and frame[pos] & 3 == 2:
+                section = _literals_section(frame[pos:pos + size])
+                if section is not None:
+                    yield section
+            pos += size
+        if last:
+            return
+
+
+def _literals_section(block):
+    b0 = block[0]
+    size_format = (b0 >> 2) & 3
+    if size_format in (0, 1):
+        h, head, bits = int.from_bytes(block[:3], "little"), 3, 10
+    elif size_format == 2:
+        h, head, bits = int.from_bytes(block[:4], "little"), 4, 14
+    else:
+        h, head, bits = int.from_bytes(block[:5], "little"), 5, 18
+    mask = (1 << bits) - 1
+    regenerated = (h >> 4) & mask
+    compressed = (h >> (4 + bits)) & mask
+    literals = block[head:head + compressed]
+    tree = tree_description_size(literals, 0)
+    return {"tree": bytes(literals[:tree]), "payload": bytes(literals[tree:]),
+            "streams": 1 if size_format == 0 else 4, "regenerated": regenerated}
+
+
 def _compressed_block(block, content):
     b0 = block[0]
     kind, size_format = b0 & 3, (b0 >> 2) & 3

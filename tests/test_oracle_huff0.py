@@ -3,6 +3,9 @@
 Decoding is checked against frames written by an independent libzstd
 (tests/golden/huff0_*.zst); encoding is checked by wrapping the oracle's
 tree description and streams in a frame that the same libzstd decodes.
+Table construction (Zstd's HUF_buildCTable_wksp and HUF_writeCTable_wksp,
+which the reference calls) is checked byte for byte against the tree
+descriptions libzstd wrote for known histograms (tests/golden/huff0_tables.json).
 """
 import json
 from pathlib import Path
@@ -16,6 +19,31 @@ from zstd_frames import huffman_frame, literal_blocks
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 MANIFEST = json.loads((GOLDEN / "huff0_vectors.json").read_text())["vectors"]
+TABLES = json.loads((GOLDEN / "huff0_tables.json").read_text())
+
+
+def table_counts(case):
+    counts = np.zeros(256, dtype=np.uint32)
+    for symbol, count in case["counts"]:
+        counts[symbol] = count
+    return counts
+
+
+def test_table_fixture_covers_the_construction_paths():
+    cases = TABLES["cases"]
+    assert len(cases) >= 100
+    assert sum(c["weights"] == "fse" for c in cases) >= 40       # FSE-compressed weights
+    assert sum(c["weights"] == "direct" for c in cases) >= 20    # 4-bit weights
+    assert sum(c["limited"] for c in cases) >= 20                # HUF_setMaxHeight at work
+    assert {c["max_bits"] for c in cases} >= set(range(1, 12))
+    # tied counts among symbols that share a sort bucket
+    assert any(len({n for _, n in c["counts"]}) < len(c["counts"]) for c in cases)
+
+
+def test_table_construction_matches_libzstd():
+    for case in TABLES["cases"]:
+        table = oracle.Huff0Table.from_counts(table_counts(case), max_bits=case["max_bits"])
+        assert table.header().hex() == case["header"], case["source"]
 
 
 def zstd_decompress(frame, size):
@@ -79,22 +107,31 @@ def test_encoder_output_is_accepted_by_libzstd(seed):
     assert reread.decode4x(payload, size) == data.tobytes()
 
 
-def test_length_limited_code_is_optimal_on_small_alphabets():
-    # brute force over all complete length assignments for 4 symbols
+def test_unlimited_code_is_optimal_and_limited_code_complete():
+    # without a binding limit Zstd's tree is a Huffman tree: brute force over
+    # every complete length assignment of 5 symbols; with one, the code
+    # still fills the Kraft sum exactly and respects the limit
     import itertools
     rng = np.random.default_rng(3)
-    for _ in range(20):
+    for _ in range(40):
         counts = np.zeros(256, dtype=np.uint32)
-        counts[:4] = rng.integers(1, 1000, 4)
-        limit = int(rng.integers(2, 4))
-        table = oracle.Huff0Table.from_counts(counts, max_bits=limit)
-        lengths = table.codes()[0][:4].astype(int)
+        counts[:5] = rng.integers(1, 1000, 5)
+        table = oracle.Huff0Table.from_counts(counts, max_bits=12)
+        lengths = table.codes()[0][:5].astype(int)
         best = min(
-            sum(int(c) * l for c, l in zip(counts[:4], ls))
-            for ls in itertools.product(range(1, limit + 1), repeat=4)
+            sum(int(c) * l for c, l in zip(counts[:5], ls))
+            for ls in itertools.product(range(1, 5), repeat=5)
             if sum(2.0 ** -l for l in ls) == 1.0
         )
-        assert sum(int(c) * l for c, l in zip(counts[:4], lengths)) == best
+        assert sum(int(c) * l for c, l in zip(counts[:5], lengths)) == best
+    for _ in range(40):
+        counts = np.zeros(256, dtype=np.uint32)
+        n = int(rng.integers(3, 60))
+        counts[:n] = (0.5 ** np.arange(n) * 2 ** 24).astype(np.uint32) + 1   # deep unconstrained tree
+        limit = int(rng.integers(int(np.ceil(np.log2(n))), 12))
+        lengths = oracle.Huff0Table.from_counts(counts, max_bits=limit).codes()[0][:n].astype(int)
+        assert lengths.max() <= limit and lengths.min() >= 1
+        assert sum(2.0 ** -int(l) for l in lengths) == 1.0
 
 
 def test_decoder_rejects_corrupt_streams():
