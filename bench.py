@@ -505,7 +505,7 @@ def main():
             return 2
         return model_benchmark(args)
     if args.gpus != 1:
-        print("bench.py measures one GPU: decode needs no collective and this build runs on one device; "
+        print("bench.py measures one GPU: decode needs no collective and the library runs on one device; "
               "run with --gpus 1.", file=sys.stderr)
         return 2
 
