@@ -255,7 +255,7 @@ __device__ __forceinline__ void fetch(const TileInfo& ti, uint32_t lane, Fetch<E
 }
 
 // One LUT step at the head of the window w0..w3: returns the entry (byte
-// count in bits 29-31 of .x; the bytes, first lowest and zeros above them,
+// count in bits 27-29 of .x; the bytes, first lowest and zeros above them,
 // in .y) and shifts the window by the consumed bits.
 template <bool LONG, bool ESC>
 __device__ __forceinline__ uint2 lut_step(const uint32_t* lut, uint32_t& w0, uint32_t& w1, uint32_t& w2,
@@ -326,12 +326,17 @@ __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, L
                 if (LONG) w3 = funnel(w3, 0u, s);
             }
         }
-        // bit: staging bit position of the next byte (8 x its index)
-        uint32_t bit = 8 * at;
-        const uint32_t stop = 8 * (at + count);
+        // bit: 8 x the LDS byte address of the next byte (the staging area
+        // is 16-byte aligned, so bit & 31 is its place in its dword); LDS
+        // addresses stay below 2^17, so bit stays below 2^20
+        typedef __attribute__((address_space(3))) uint32_t lds_u32;
+        const uint32_t base = static_cast<uint32_t>(
+            reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)stage));
+        uint32_t bit = 8 * (base + at);
+        const uint32_t stop = bit + 8 * count;
         do {
             const uint2 e = lut_step<LONG, ESC>(lut, w0, w1, w2, w3);
-            uint32_t* dst = reinterpret_cast<uint32_t*>(stage) + __builtin_amdgcn_ubfe(bit, 5u, 27u);
+            lds_u32* dst = (lds_u32*)(uintptr_t)((bit >> 3) & ~3u);
             // The entry's bytes in this dword, and the ones past it: one
             // 64-bit shift (two 32-bit shifts and a negation before).
             const uint64_t both = static_cast<uint64_t>(e.y) << (bit & 31u);
@@ -345,7 +350,7 @@ __device__ __forceinline__ void stage_tile(const TileInfo& ti, const Fetch<ES, L
             // returned staging data in place of the LUT entry, now and then;
             // waiting here costs under 1 % of the decode time.
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-            bit += e.x >> (NZ_ENTRY_COUNT - 3);   // 8 x the byte count (bits 5-28 of an entry are zero)
+            bit += e.x >> (NZ_ENTRY_COUNT - 3);   // 8 x the byte count (bits 5-26 of an entry are zero)
         } while (bit < stop);
     }
     wave_lds_sync();

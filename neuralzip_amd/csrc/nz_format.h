@@ -53,16 +53,17 @@
 //   then T escape token entries (one word)
 // A primary entry decodes every whole token that fits the 12-bit prefix, up
 // to four exponent bytes b0..b3:
-//   word 0: (32 - consumed bits) | byte count << 29
+//   word 0: (32 - consumed bits) | byte count << 27
 //   word 1: b0 | b1 << 8 | b2 << 16 | b3 << 24
 // (consumed 1..12; byte count 1..4, 0 marks an escape). Word 0 is the
 // decoder's funnel-shift operand as it stands (the shift reads the low five
-// bits) and word 1 is stored as one dword.
-// Escape token entry: b0 | b1 << 8 | byte count << 29.
+// bits), and its top byte is 8 x the byte count, which one byte-select add
+// (SDWA) adds to a bit position; word 1 is stored as one dword.
+// Escape token entry: b0 | b1 << 8 | byte count << 27.
 #define NZ_LUT_HEADER 4
 #define NZ_ESC_RECORD 6
 #define NZ_ENTRY_SHIFT_MASK 31u
-#define NZ_ENTRY_COUNT 29
+#define NZ_ENTRY_COUNT 27
 #define NZ_ENTRY_MAX_BYTES 4
 #define NZ_LUT_MAX_WORDS (NZ_LUT_HEADER + 2 * NZ_LUT_ENTRIES + NZ_ESC_RECORD * 56 + 512)
 
