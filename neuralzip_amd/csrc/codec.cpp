@@ -138,15 +138,18 @@ int build_tree(Node* node, int max_symbol) {
 unsigned limit_height(Node* node, int last, unsigned target) {
     const unsigned largest = node[last].bits;
     if (largest <= target) return largest;
-    const int base_cost = 1 << (largest - target);
-    int cost = 0, n = last;
+    // 64-bit: with histograms totalling up to 2^30 a tree can be 42 deep,
+    // where Zstd's 32-bit shifts (sized for 128 KiB blocks) would overflow
+    const int64_t base_cost = int64_t(1) << (largest - target);
+    int64_t wide = 0;
+    int n = last;
     while (node[n].bits > target) {
-        cost += base_cost - (1 << (largest - node[n].bits));
+        wide += base_cost - (int64_t(1) << (largest - node[n].bits));
         node[n].bits = static_cast<uint8_t>(target);
         --n;
     }
     while (node[n].bits == target) --n;
-    cost >>= (largest - target);   // a multiple of base_cost before the shift
+    int cost = static_cast<int>(wide >> (largest - target));   // a multiple of base_cost before the shift
     constexpr uint32_t kNone = 0xF0F0F0F0u;
     uint32_t rank_last[12 + 2];
     std::fill(std::begin(rank_last), std::end(rank_last), kNone);

@@ -735,15 +735,17 @@ static int huf_zstd_tree(const uint32_t* counts, int max_symbol, huf_node* node)
 static void huf_zstd_limit(huf_node* node, int last, int target) {
     const int largest = node[last].bits;
     if (largest <= target) return;
-    const int base_cost = 1 << (largest - target);
-    int total = 0, n = last;
+    /* 64-bit: trees of histograms totalling up to 2^30 can be 42 deep */
+    const int64_t base_cost = (int64_t)1 << (largest - target);
+    int64_t wide = 0;
+    int n = last;
     while (node[n].bits > target) {
-        total += base_cost - (1 << (largest - node[n].bits));
+        wide += base_cost - ((int64_t)1 << (largest - node[n].bits));
         node[n].bits = target;
         --n;
     }
     while (node[n].bits == target) --n;
-    total >>= largest - target;
+    int total = (int)(wide >> (largest - target));
     const uint32_t none = 0xF0F0F0F0u;
     uint32_t rank_last[HUF_MAX_BITS + 2];
     for (int k = 0; k < HUF_MAX_BITS + 2; ++k) rank_last[k] = none;

@@ -91,6 +91,21 @@ def test_huff0_build_matches_oracle_on_random_histograms(seed):
         assert huff0.build_codebook_from_counts(counts, prior_count=prior, max_bits=max_bits).codebook == expected
 
 
+def test_huff0_build_limits_the_deepest_trees():
+    # Fibonacci counts totalling just under 2^30 give an unconstrained tree
+    # 41 levels deep, past the 32-bit shifts of Zstd's 128 KiB blocks
+    fib = [1, 1]
+    while sum(fib) + fib[-1] + fib[-2] < (1 << 30) - 1:
+        fib.append(fib[-1] + fib[-2])
+    counts = np.zeros(256, dtype=np.int64)
+    counts[:len(fib)] = fib
+    for max_bits in (6, 9, 12):
+        book = huff0.build_codebook_from_counts(counts, prior_count=0, max_bits=max_bits)
+        assert book.codebook == oracle.Huff0Table.from_counts(counts.astype(np.uint32), max_bits).header()
+        lengths = oracle.Huff0Table.from_header(book.codebook).codes()[0][:len(fib)]
+        assert lengths.max() == max_bits and sum(2.0 ** -int(l) for l in lengths) == 1.0
+
+
 def test_huff0_headers_small_alphabets_use_direct_weights():
     counts = np.zeros(256, dtype=np.int64)
     counts[:20] = np.arange(1, 21) ** 3
