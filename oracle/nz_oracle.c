@@ -7,7 +7,10 @@
  *                                       native/common.h:198-257
  *   - NZM1 mixed pair/singleton code    native/mixed_huffman.h:1-240
  *   - Huff0 singleton code              native/codebooks.h (delegates to Zstd;
- *                                       restated from RFC 8878 4.1 and 4.2)
+ *                                       formats restated from RFC 8878 4.1
+ *                                       and 4.2, table construction and the
+ *                                       tree-description writer from Zstd's
+ *                                       huf_compress.c and fse_compress.c)
  *   - threaded aligned-chunk decode     native/decode_queue.h:1-113,
  *                                       native/common.h:134-185
  * It is written for clarity; its decode loops follow the reference's own
