@@ -57,6 +57,15 @@ def test_huff0_build_matches_libzstd_tables():
         assert book.codebook.hex() == case["header"], case["source"]
 
 
+def test_huff0_header_writer_matches_libzstd():
+    # the writer alone: the code lengths of each libzstd tree description
+    # are written back to the same bytes
+    tables = json.loads((Path(__file__).resolve().parent / "golden" / "huff0_tables.json").read_text())["cases"]
+    for case in tables:
+        lengths = oracle.Huff0Table.from_header(bytes.fromhex(case["header"])).codes()[0]
+        assert huff0.huff0_header_from_lengths(lengths).hex() == case["header"], case["source"]
+
+
 @pytest.mark.parametrize("seed", range(3))
 def test_huff0_build_matches_oracle_on_random_histograms(seed):
     # scaled histograms (totals above 2^30), priors and every limit
