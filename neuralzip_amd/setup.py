@@ -19,8 +19,10 @@ samples in fewer bytes. Every tensor also gets a singleton code of its
 pooled counts, the fallback for a tensor whose chunking no longer matches.
 Identical codebooks are stored once unless shared codebooks are disabled.
 
-Setups pickle (protocol 5) with the reference's class and attribute names,
-so either library reads the other's setup files.
+Setups pickle (protocol 5) with the reference's class paths
+(neuralzip.setup.NeuralZipSetup, neuralzip.setup.NeuralZipSetupReport,
+neuralzip.payloads.CodebookPayload) and attribute names, so either library
+reads the other's setup files.
 """
 import io
 import pickle
@@ -68,6 +70,24 @@ class _SetupUnpickler(pickle.Unpickler):
         if module == "builtins" and name in ("frozenset", "set", "tuple", "bytearray", "complex"):
             return getattr(__import__("builtins"), name)
         raise pickle.UnpicklingError(f"Setup pickles may not reference {module}.{name}.")
+
+
+class _SetupPickler(pickle._Pickler):
+    """Protocol-5 pickler that names the setup and payload classes by the
+    reference's module paths, as the reference's own pickle.dump of a setup
+    does (setup.py:75-80); everything else is pickled as usual. It builds on
+    the pure-Python pickler because only there can a subclass decide which
+    module path is written for a class (the C pickler checks that the path
+    imports to the same object)."""
+
+    def save_global(self, obj, name=None):
+        path = _REFERENCE_PATHS.get(obj) if isinstance(obj, type) else None
+        if path is None:
+            return super().save_global(obj, name)
+        for text in path:
+            self.save(text)
+        self.write(pickle.STACK_GLOBAL)
+        self.memoize(obj)
 
 
 @dataclass(eq=False)
@@ -316,7 +336,9 @@ class NeuralZipSetup:
     def save(self, path):
         target = Path(path)
         target.parent.mkdir(parents=True, exist_ok=True)
-        target.write_bytes(pickle.dumps(self, protocol=5))
+        buffer = io.BytesIO()
+        _SetupPickler(buffer, protocol=5).dump(self)
+        target.write_bytes(buffer.getvalue())
         return target
 
     @classmethod
@@ -328,3 +350,11 @@ class NeuralZipSetup:
         if isinstance(value, cls) and hasattr(value, "chunk_codebooks"):
             return value
         raise TypeError("Expected a current chunk-level NeuralZip setup.")
+
+
+# the classes a setup pickle holds, by the module path the reference gives them
+_REFERENCE_PATHS = {
+    NeuralZipSetup: ("neuralzip.setup", "NeuralZipSetup"),
+    NeuralZipSetupReport: ("neuralzip.setup", "NeuralZipSetupReport"),
+    CodebookPayload: ("neuralzip.payloads", "CodebookPayload"),
+}
