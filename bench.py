@@ -56,8 +56,9 @@ def make_tensors(seed=1):
     return tensors
 
 
-def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
-    """Oracle storage decode (decode_queue.h semantics) of the same tensors."""
+def _storage_specs(tensors, setup):
+    """The workload's storage v2 archive, as decode specs for the oracle and
+    for the product's native decoder, plus the decoded byte count."""
     import oracle
     from neuralzip_amd.compressor import NeuralZipCompressor
     from neuralzip_amd.storage import unpack_storage
@@ -65,14 +66,24 @@ def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
     codebooks, payloads = unpack_storage(blob, metadata)
     tables = {b.codebook_id: (oracle.MixedTable(bytes(b.codebook), bytes(b.vocab)) if b.mode == "mixed_huffman"
                               else oracle.Huff0Table.from_header(bytes(b.codebook))) for b in codebooks}
-    specs = [(t.element_size, bool(t.bit_reorder), t.numel,
-              tuple(tuple((c.mode, bytes(c.payload), c.symbol_count, tables.get(c.codebook_id)) for c in g.chunks)
-                    for g in t.groups)) for t in payloads]
+    oracle_specs = [(t.element_size, bool(t.bit_reorder), t.numel,
+                     tuple(tuple((c.mode, bytes(c.payload), c.symbol_count, tables.get(c.codebook_id))
+                                 for c in g.chunks) for g in t.groups)) for t in payloads]
+    product = NeuralZipCompressor()
+    product.load_codebooks(codebooks)
+    product_specs = [product._decode_spec(t) for t in payloads]
     decoded = sum(t.numel * t.element_size for t in payloads)
+    return oracle_specs, product_specs, decoded
+
+
+def _timed_decodes(decode, tensors, decoded, reps, warmups, budget_s):
+    """Median and interquartile range of GB/s over timed calls of decode()
+    (after `warmups` untimed ones, at least 3 timed within `budget_s`); the
+    last call's output must be the workload's words."""
     times, start = [], time.perf_counter()
     for rep in range(warmups + reps):
         t0 = time.perf_counter()
-        out = oracle.decompress_many(specs, threads=threads)
+        out = decode()
         dt = time.perf_counter() - t0
         if rep >= warmups:
             times.append(dt)
@@ -80,13 +91,34 @@ def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0):
             break
     for (name, t), data in zip(tensors.items(), out):
         if bytes(data) != t.view(torch.uint8).numpy().tobytes():
-            raise RuntimeError(f"oracle decode of {name} is not bit-exact")
+            raise RuntimeError(f"CPU decode of {name} is not bit-exact")
     rates = sorted(decoded / t / 1e9 for t in times)
     q1, _, q3 = statistics.quantiles(rates, n=4) if len(rates) > 1 else (rates[0],) * 3
-    return {"value": round(statistics.median(rates), 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "iqr": [round(q1, 3), round(q3, 3)],
-            "sample": f"full workload, {len(times)} timed decodes (median, interquartile range) after {warmups} "
+    return round(statistics.median(rates), 3), [round(q1, 3), round(q3, 3)], len(times)
+
+
+def cpu_baseline(tensors, setup, threads, reps=9, warmups=4, budget_s=25.0, specs=None):
+    """The oracle's storage decode (decode_queue.h semantics) of the same
+    tensors on `threads` threads."""
+    import oracle
+    oracle_specs, _, decoded = specs or _storage_specs(tensors, setup)
+    value, iqr, n = _timed_decodes(lambda: oracle.decompress_many(oracle_specs, threads=threads), tensors, decoded,
+                                   reps, warmups, budget_s)
+    return {"value": value, "unit": "GB/s", "cores": threads, "kind": "port", "iqr": iqr,
+            "sample": f"full workload, {n} timed decodes (median, interquartile range) after {warmups} "
                       f"warmups, {decoded} bytes decoded each"}
+
+
+def product_cpu_decode(tensors, setup, threads, reps=9, warmups=2, budget_s=15.0, specs=None):
+    """The product's own threaded storage decoder (nz_storage_decompress, the
+    CPU path a checkpoint load takes) on the same archive."""
+    from neuralzip_amd import huff0
+    _, product_specs, decoded = specs or _storage_specs(tensors, setup)
+    value, iqr, n = _timed_decodes(lambda: huff0.decompress_mixed_streams_many(product_specs, threads=threads),
+                                   tensors, decoded, reps, warmups, budget_s)
+    return {"value": value, "unit": "GB/s", "threads": threads, "iqr": iqr,
+            "what": "nz_storage_decompress (product CPU storage decoder), same archive",
+            "sample": f"{n} timed decodes after {warmups} warmups"}
 
 
 def host_description():
@@ -206,14 +238,18 @@ def random_model(kind, device, dtype=torch.bfloat16, seed=1):
 
 def time_generate(model, ids, new_tokens):
     """(decode-phase seconds for new_tokens - 1 tokens, generated ids): the
-    time of generating new_tokens minus the time of generating one."""
+    time of generating new_tokens minus the time of generating one, each
+    taken with a pair of HIP events on the current stream around the call."""
     def run(n):
+        stream = torch.cuda.current_stream()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        begin.record(stream)
         out = model.generate(ids, max_new_tokens=n, min_new_tokens=n, do_sample=False, use_cache=True,
                              pad_token_id=0)
+        end.record(stream)
         torch.cuda.synchronize()
-        return time.perf_counter() - t0, out
+        return begin.elapsed_time(end) * 1e-3, out
     run(2)   # warm
     first, _ = run(1)
     full, out = run(new_tokens)
@@ -261,14 +297,17 @@ def graph_generate(model, ids, new_tokens, runtime=None):
         # a spin kernel on each side of the replays marks them in kernel traces
         torch.cuda._sleep(1000)
         torch.cuda.synchronize(device)
-        t0 = time.perf_counter()
+        stream = torch.cuda.current_stream(device)
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
         for _ in range(replays):
             graph.replay()
             generated.append(out.clone())
             token.copy_(out)
             position += 1
+        end.record(stream)
         torch.cuda.synchronize(device)
-        seconds = time.perf_counter() - t0
+        seconds = begin.elapsed_time(end) * 1e-3
         torch.cuda._sleep(1000)
     del graph
     return seconds, replays, torch.cat(generated, dim=1)
@@ -472,6 +511,33 @@ def model_summary(line):
             "peak_allocated_neuralzip_gib": line["config"]["peak_allocated_neuralzip_gib"]}
 
 
+def trace_summary(path, kernel="nz_decode_kernel<2, true, false, false>", steps=20):
+    """Summary of a rocprofv3 kernel trace (CSV) of the default bench run: the
+    durations of the last `steps` dispatches whose kernel name contains
+    `kernel` (the timed steps, which end the run) and their mean, beside all
+    of its dispatches. Prints JSON."""
+    import csv
+    rows = []
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if kernel in row.get("Kernel_Name", ""):
+                rows.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]),
+                             int(row.get("Grid_Size_X") or row.get("Grid_Size") or 0),
+                             int(row.get("Workgroup_Size_X") or row.get("Workgroup_Size") or 0)))
+    rows.sort()
+    if len(rows) < steps:
+        raise SystemExit(f"{path}: {len(rows)} dispatches of {kernel}, fewer than {steps}")
+    timed = rows[-steps:]
+    us = [(end - start) / 1e3 for start, end, _, _ in timed]
+    every = [(end - start) / 1e3 for start, end, _, _ in rows]
+    print(json.dumps({"kernel": kernel, "dispatches": len(rows), "mean_us_all": round(statistics.mean(every), 3),
+                      "timed_dispatches": steps, "timed_grid": sorted({g for _, _, g, _ in timed}),
+                      "timed_workgroup": sorted({w for _, _, _, w in timed}),
+                      "timed_mean_us": round(statistics.mean(us), 3), "timed_us": [round(u, 1) for u in us],
+                      "span_of_timed_us": round((timed[-1][1] - timed[0][0]) / 1e3, 1)}), flush=True)
+    return 0
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -496,7 +562,12 @@ def main():
     parser.add_argument("--no-graph", action="store_true", help="model benchmark: eager generation only")
     parser.add_argument("--no-model", action="store_true",
                         help="default run: leave out the Llama-3-8B-shape bs=1 tok/s part of the line")
+    parser.add_argument("--trace-summary", default=None, metavar="KERNEL_TRACE_CSV",
+                        help="summarize a rocprofv3 kernel trace of a default run: the decode kernel's last "
+                             "--steps dispatches (the timed steps)")
     args = parser.parse_args()
+    if args.trace_summary:
+        return trace_summary(args.trace_summary, steps=args.steps)
     if args.copy_calibration:
         return copy_calibration()
     if args.model:
@@ -610,11 +681,17 @@ def main():
     baseline = None
     if not args.no_cpu_baseline:
         threads = min(os.cpu_count() or 1, 16)
-        baseline = cpu_baseline(tensors, setup, threads)
+        specs = _storage_specs(tensors, setup)
+        baseline = cpu_baseline(tensors, setup, threads, specs=specs)
         log(f"cpu baseline {baseline['value']} GB/s on {threads} threads")
-        single = cpu_baseline(tensors, setup, 1, budget_s=20.0)
+        single = cpu_baseline(tensors, setup, 1, budget_s=20.0, specs=specs)
         log(f"cpu baseline {single['value']} GB/s on 1 thread")
         baseline["single_thread"] = {k: single[k] for k in ("value", "unit", "iqr", "sample")}
+        native = product_cpu_decode(tensors, setup, threads, specs=specs)
+        log(f"product CPU storage decode {native['value']} GB/s on {threads} threads")
+        baseline["product_native"] = native
+        baseline["reference_archived"] = {"value": 5.62, "unit": "GB/s", "threads": 12,
+                                          "what": "the reference's published CPU Huff0 decode figure (other host)"}
         baseline["host"] = host_description()
 
     line = {
