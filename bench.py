@@ -432,7 +432,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
         # the same compressed weights with fused decode-matvec products for
         # one-token steps: graph-replayed steps only; not bit-identical to the
         # GEMM, so the tokens follow bf16 only for a while
-        runtime = runtime.replace(matvec_tokens=1)
+        runtime = runtime.replace(matvec_tokens=1, graphs_released=True)   # graph_generate deleted its graph
         torch.cuda.empty_cache()
         fused = graph_generate(model, ids, new_tokens, runtime)
         f_ms = fused[0] / fused[1] * 1e3

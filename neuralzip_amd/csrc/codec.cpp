@@ -50,7 +50,8 @@ struct Node {
 
 constexpr int kBuckets = 192;
 constexpr uint32_t kLogBucketsBegin = kBuckets - 1 - 32 - 1;   // 158
-constexpr uint32_t kDistinctBelow = kLogBucketsBegin + 7;       // 158 + highbit(158) = 166
+constexpr uint32_t kDistinctBelow = kLogBucketsBegin + 7;       // 158 + highbit(158) = 158 + 7 = 165
+static_assert(kLogBucketsBegin == 158 && kDistinctBelow == 165, "Zstd's bucket bounds");
 constexpr int kFirstInternal = 256;
 
 uint32_t bucket_of(uint32_t count) {
@@ -99,8 +100,8 @@ void sort_symbols(const uint32_t* counts, int max_symbol, Node* leaf) {
         n.count = counts[s];
         n.symbol = static_cast<uint8_t>(s);
     }
-    // only the shared buckets (from index 165, which also holds counts
-    // 166-255) can be out of order
+    // only the shared buckets can be out of order: from index 165 on, where
+    // bucket 165 holds every count from 165 to 255 (highbit 7 + 158)
     for (uint32_t b = kDistinctBelow; b < kBuckets - 1; ++b) {
         const int size = static_cast<int>(end[b] - first[b]);
         if (size > 1) quick_sort(leaf + first[b], 0, size - 1);

@@ -536,6 +536,7 @@ class NeuralZipRuntime:
         self._pending = None   # (unit name, event) decoded ahead on the side stream
         self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
         self._side_off = False  # graph_capture() decodes on the compute stream only
+        self._captured = False  # graph_capture() was used: graphs may hold this runtime's buffers
         self._matvec, self._matvec_blocks, self._partials = {}, frozenset(), None
         self._fused = set()    # blocks whose current call runs the fused products
         if self.matvec_tokens:
@@ -573,8 +574,21 @@ class NeuralZipRuntime:
         self._observation = None   # (input, version, [module names called with it])
         self._outputs = {}         # module name -> (input, version, output) computed with its group
         if plans:
-            need = max(2 * plan.n_tiles for plan in plans.values()) * self.matvec_tokens
-            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+            # one buffer for every product the runtime may form, sized now and
+            # never replaced: a graph captured with it keeps its address
+            self._partials = torch.empty(self._partials_bound(plans, members), dtype=torch.float32,
+                                         device=self.device)
+
+    def _partials_bound(self, plans, members):
+        """Partial sums of the largest product a forward can form: one Linear,
+        or a learned group of up to MATVEC_MAX_WEIGHTS Linears of one block,
+        dtype and width (a group's product has all its members' tiles)."""
+        tiles = defaultdict(list)
+        for name, plan in plans.items():
+            block, spec, cols, _ = members[name]
+            tiles[(block, spec.name, cols)].append(plan.n_tiles)
+        largest = max(sum(sorted(counts, reverse=True)[:_native.MATVEC_MAX_WEIGHTS]) for counts in tiles.values())
+        return 2 * largest * self.matvec_tokens
 
     def _compute_units(self):
         return torch.cuda.get_device_properties(self.device).multi_processor_count
@@ -588,9 +602,14 @@ class NeuralZipRuntime:
 
     def _learn_group(self, names):
         """After Linears `names` were called with one input, in this order:
-        one fused product for all of them from the first one's call on."""
+        one fused product for all of them from the first one's call on.
+        Nothing is learned while the stream is being captured: planning
+        allocates and copies, which a capture must not record; the captured
+        forward keeps the per-Linear products and a later eager call learns."""
         first = names[0]
         if first in self._group_plans or first in self._group_tried:
+            return
+        if torch.cuda.is_current_stream_capturing():
             return
         self._group_tried.add(first)
         info = [self._matvec_members[n] for n in names]
@@ -603,11 +622,8 @@ class NeuralZipRuntime:
             plan = self._decoder.prepare_matvec(self.store, [i[3] for _, i in ordered], spec, cols)
         except (_native.NativeError, ValueError):
             return
-        # a group's product has the tiles of all its members: the partial-sum
-        # buffer, sized for the largest single Linear, may be too small
-        need = 2 * plan.n_tiles * self.matvec_tokens
-        if self._partials.numel() < need:
-            self._partials = torch.empty(need, dtype=torch.float32, device=self.device)
+        if 2 * plan.n_tiles * self.matvec_tokens > self._partials.numel():
+            return   # cannot happen with the bound of _partials_bound; never reallocate
         self._group_plans[first] = (plan, tuple(n for n, _ in ordered),
                                     tuple(self.model.get_submodule(n) for n, _ in ordered))
 
@@ -760,6 +776,12 @@ class NeuralZipRuntime:
                 ahead = self._schedule_args[following]
         _native.decode_schedule(inline, ahead, wait, ready, done, stream, self._side_handle)
         self._pending = (following, done) if following is not None else None
+        if torch.is_grad_enabled():
+            # the decodes overwrite workspace slots behind autograd's back: a
+            # new version makes a backward that saved an earlier block's weight
+            # fail loudly instead of reading the bytes of a later block
+            for workspace in self.workspaces.values():
+                torch.autograd.graph.increment_version(workspace)
 
     def drain(self):
         """Order the compute stream after any pending side-stream decode."""
@@ -768,11 +790,20 @@ class NeuralZipRuntime:
                                     None)
             self._pending = None
 
-    def replace(self, **options):
+    def replace(self, *, graphs_released=False, **options):
         """A runtime over the same model and export with some options changed
         (prefetch, matvec_tokens, decode_slots, granularity); the weights stay
         compressed. This runtime's hooks and fused forwards are removed, and
-        it must not be used afterwards."""
+        it must not be used afterwards.
+
+        Its device buffers (workspaces, descriptors, the compressed store when
+        the new runtime does not take it over) are freed, and HIP graphs
+        captured through it read and write them. After a graph_capture() the
+        call is refused unless `graphs_released` says those graphs have been
+        deleted."""
+        if self._captured and not graphs_released:
+            raise RuntimeError("HIP graphs were captured with this runtime and read its device buffers, which "
+                               "replace() frees: delete them, then call replace(graphs_released=True).")
         self.drain()
         torch.cuda.current_stream(self.device).synchronize()
         for handle in self._hook_handles:
@@ -818,6 +849,7 @@ class NeuralZipRuntime:
         self.drain()
         self._wrap = False
         self._side_off = not prefetch
+        self._captured = True
         try:
             yield self
         finally:
