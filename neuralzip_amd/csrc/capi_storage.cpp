@@ -6,6 +6,7 @@
 #include <cstring>
 #include <string>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 #include "capi_internal.hpp"
@@ -42,16 +43,31 @@ void extract(const nz_storage_tensor& t, uint64_t start, uint64_t length, uint8_
 
 // common.h:198-257: interleave lanes and undo the reorder of the
 // byte-aligned-exponent layouts.
-void restore(const uint8_t* const* lanes, uint64_t length, unsigned es, bool reorder, uint8_t* out) {
+// Words from their byte lanes (common.h:198-257): lane k is byte k of each
+// word; with the reorder the exponent byte (the last lane) and the sign (top
+// bit of the lane below) move back: bits m..m+7 of the exponent and bit m+8
+// of the sign, m = 8 * es - 9.
+template <unsigned ES, bool REORDER>
+void restore_words(const uint8_t* const* lanes, uint64_t length, uint8_t* __restrict out) {
+    using Word = std::conditional_t<ES == 2, uint16_t, uint32_t>;
+    constexpr unsigned m = ES * 8 - 9;
+    // the lane pointers in locals: byte stores could otherwise alias the array
+    const uint8_t* __restrict l0 = lanes[0];
+    const uint8_t* __restrict l1 = lanes[1];
+    const uint8_t* __restrict l2 = ES == 4 ? lanes[2] : lanes[0];
+    const uint8_t* __restrict l3 = ES == 4 ? lanes[3] : lanes[0];
     for (uint64_t i = 0; i < length; ++i) {
-        uint32_t v = 0;
-        for (unsigned k = 0; k < es; ++k) v |= uint32_t(lanes[k][i]) << (8 * k);
-        if (reorder) {
-            const unsigned m = es * 8 - 9;
-            v = (v & ((1u << m) - 1u)) | ((v << 8) & (1u << (m + 8))) | ((v >> 1) & (0xFFu << m));
-        }
-        for (unsigned k = 0; k < es; ++k) out[i * es + k] = static_cast<uint8_t>(v >> (8 * k));
+        uint32_t v = uint32_t(l0[i]) | uint32_t(l1[i]) << 8;
+        if (ES == 4) v |= uint32_t(l2[i]) << 16 | uint32_t(l3[i]) << 24;
+        if (REORDER) v = (v & ((1u << m) - 1u)) | ((v << 8) & (1u << (m + 8))) | ((v >> 1) & (0xFFu << m));
+        const Word w = static_cast<Word>(v);
+        std::memcpy(out + i * ES, &w, ES);
     }
+}
+
+void restore(const uint8_t* const* lanes, uint64_t length, unsigned es, bool reorder, uint8_t* out) {
+    if (es == 2) (reorder ? restore_words<2, true> : restore_words<2, false>)(lanes, length, out);
+    else (reorder ? restore_words<4, true> : restore_words<4, false>)(lanes, length, out);
 }
 
 constexpr size_t kSharedMetadata = 25;   // direct_storage.h:1, payloads.py:5-11

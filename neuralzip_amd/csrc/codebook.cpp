@@ -389,6 +389,15 @@ Codebook build_codebook(const uint8_t* header, size_t header_size, const uint8_t
     check_kraft(book);
     assign_canonical(book);
     build_lut(book);
+    if (book.mixed)   // the CPU storage decoder's table (NZM1 frames use the canonical codes)
+        book.multi = multi_token_table(NZ_LUT_BITS, [&](uint32_t prefix, uint32_t* bytes, unsigned* width) {
+            const uint32_t e = book.single[prefix];
+            if (!e) return 0u;
+            const unsigned token = e & 0xFFFFu;
+            *bytes = book.token_bytes[token];
+            *width = Codebook::token_width(token);
+            return e >> 16;
+        });
     return book;
 }
 

@@ -39,11 +39,44 @@ struct Codebook {
     unsigned longest = 0;
     std::vector<uint32_t> lut;          // device LUT image (nz_format.h)
     std::vector<uint32_t> single;       // 12-bit prefix -> token | length << 16 (0: longer code)
+    std::vector<uint64_t> multi;        // NZM1 only: 12-bit prefix -> whole tokens (multi_token_table)
     uint64_t vocab_bytes = 0;
 
     unsigned token_count() const { return static_cast<unsigned>(lengths.size()); }
     static unsigned token_width(unsigned token) { return token < 256 ? 1u : 2u; }
 };
+
+// Multi-token decode table of a prefix code: each `log`-bit prefix (MSB
+// first) maps to the whole tokens that start it, up to four tokens and four
+// bytes, as bytes (first lowest) | bits << 32 | n_bytes << 40 | n_tokens << 44;
+// 0 when no whole token fits the prefix. `single(prefix, &bytes, &width)`
+// returns the length of the one token a prefix starts with (0: longer than
+// `log`), its bytes and their count.
+template <typename Single>
+std::vector<uint64_t> multi_token_table(unsigned log, Single single) {
+    std::vector<uint64_t> table(size_t(1) << log, 0);
+    const uint32_t mask = (1u << log) - 1;
+    for (uint32_t prefix = 0; prefix <= mask; ++prefix) {
+        unsigned used = 0, n_bytes = 0, n_tokens = 0;
+        uint32_t value = 0;
+        while (n_tokens < 4) {
+            uint32_t bytes = 0;
+            unsigned width = 0;
+            const unsigned len = single((prefix << used) & mask, &bytes, &width);
+            if (!len || used + len > log || n_bytes + width > 4) break;
+            value |= bytes << (8 * n_bytes);
+            n_bytes += width;
+            used += len;
+            ++n_tokens;
+        }
+        if (n_tokens)
+            table[prefix] = value | uint64_t(used) << 32 | uint64_t(n_bytes) << 40 | uint64_t(n_tokens) << 44;
+    }
+    return table;
+}
+inline unsigned multi_bits(uint64_t e) { return static_cast<unsigned>(e >> 32) & 0xFFu; }
+inline unsigned multi_bytes(uint64_t e) { return static_cast<unsigned>(e >> 40) & 0xFu; }
+inline unsigned multi_tokens(uint64_t e) { return static_cast<unsigned>(e >> 44) & 0xFu; }
 
 // Parses either an NZM1 header (b"NZM1" + token lengths, with vocab holding
 // the pairs) or a Huff0 tree description (RFC 8878 4.2.1). Mirrors the

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "codec.hpp"
+#include "nz_format.h"
 
 namespace nz {
 namespace {
@@ -229,32 +230,6 @@ private:
     std::vector<uint8_t>& out_;
     uint64_t acc_ = 0;
     unsigned fill_ = 0;
-};
-
-// Reads a stream from its end (RFC 8878 4.1): 64-bit window refilled
-// backwards, zero bits before the start.
-class BackReader {
-public:
-    BackReader(const uint8_t* data, size_t size) : data_(data), size_(size) {
-        if (!size || !data[size - 1]) fail(kCorruptStream, "Backward bitstream lacks its end mark.");
-        left_ = static_cast<int64_t>(size) * 8 - (8 - highbit(data[size - 1]));
-    }
-    uint32_t peek(unsigned n) const {
-        if (left_ <= 0 || n == 0) return 0;
-        const int64_t hi = (left_ + 7) >> 3;
-        uint64_t w = 0;
-        if (hi >= 8) std::memcpy(&w, data_ + hi - 8, 8);
-        else for (int64_t i = 0; i < hi; ++i) w |= uint64_t(data_[i]) << (8 * (i - hi + 8));
-        const int64_t shift = left_ - n - 8 * (hi - 8);
-        return static_cast<uint32_t>((shift >= 0 ? w >> shift : w << -shift) & ((uint64_t(1) << n) - 1));
-    }
-    void skip(unsigned n) { left_ -= n; }
-    int64_t left() const { return left_; }
-
-private:
-    const uint8_t* data_;
-    size_t size_;
-    int64_t left_;
 };
 
 // ------------------------------------------------------------ FSE weights
@@ -589,6 +564,13 @@ Huff0Tables huff0_tables(const std::array<uint8_t, 256>& lengths) {
             slot += span;
         }
     }
+    if (t.log)
+        t.multi = multi_token_table(t.log, [&](uint32_t prefix, uint32_t* bytes, unsigned* width) {
+            const uint16_t e = t.decode[prefix];
+            *bytes = e >> 8;
+            *width = 1;
+            return static_cast<unsigned>(e & 0xFF);
+        });
     return t;
 }
 
@@ -617,7 +599,24 @@ size_t huff0_encode4x(const Huff0Tables& t, const uint8_t* src, size_t n, uint8_
     return out.size();
 }
 
+// The next 64 bits of a backward stream (RFC 8878 4.1) in read order, most
+// significant first: bits [0, left) are unread and bit left - 1 comes next;
+// at least 57 bits are valid, and bits before the stream's start read as 0.
+static inline uint64_t back_window(const uint8_t* data, int64_t left) {
+    if (left <= 0) return 0;
+    const int64_t top = (left - 1) >> 3;            // the byte holding the next bit
+    uint64_t w = 0;
+    if (top >= 7) std::memcpy(&w, data + top - 7, 8);
+    else std::memcpy(reinterpret_cast<uint8_t*>(&w) + 7 - top, data, static_cast<size_t>(top) + 1);
+    return w << (8 * top + 8 - left);                // little-endian host
+}
+
+static inline void store32(uint8_t* p, uint32_t v) { std::memcpy(p, &v, 4); }
+
 void huff0_decode4x(const Huff0Tables& t, const uint8_t* src, size_t size, uint8_t* dst, size_t n) {
+    // HUF_decompress4X semantics: four streams of (n + 3) / 4 symbols (the
+    // last takes the rest), each read backwards from its end mark, and each
+    // must end exactly at its first bit
     if (n == 0) return;
     if (size < 10 || n < 6) fail(kCorruptStream, "Huff0 4X block too small.");
     size_t lens[4];
@@ -626,18 +625,39 @@ void huff0_decode4x(const Huff0Tables& t, const uint8_t* src, size_t size, uint8
     lens[3] = size - 6 - lens[0] - lens[1] - lens[2];
     const size_t segment = (n + 3) / 4;
     if (3 * segment > n) fail(kCorruptStream, "Huff0 4X block too small.");
+    const uint8_t* data[4];
+    int64_t left[4];
+    uint8_t* out[4];
+    size_t rem[4];
     const uint8_t* stream = src + 6;
     for (int k = 0; k < 4; ++k) {
-        const size_t count = k < 3 ? segment : n - 3 * segment;
-        BackReader r(stream, lens[k]);
-        uint8_t* out = dst + segment * k;
-        for (size_t i = 0; i < count; ++i) {
-            const uint16_t e = t.decode[r.peek(t.log)];
-            out[i] = static_cast<uint8_t>(e >> 8);
-            r.skip(e & 0xFF);
-        }
-        if (r.left() != 0) fail(kCorruptStream, "Huff0 stream not fully consumed.");
+        if (!lens[k] || !stream[lens[k] - 1]) fail(kCorruptStream, "Backward bitstream lacks its end mark.");
+        data[k] = stream;
+        left[k] = static_cast<int64_t>(lens[k]) * 8 - (8 - highbit(stream[lens[k] - 1]));
+        out[k] = dst + segment * k;
+        rem[k] = k < 3 ? segment : n - 3 * segment;
         stream += lens[k];
+    }
+    const unsigned shift = 64 - t.log;
+    const uint64_t* multi = t.multi.data();
+    // the four streams in turn while each has room for a four-byte store
+    while (rem[0] >= 4 && rem[1] >= 4 && rem[2] >= 4 && rem[3] >= 4) {
+        for (int k = 0; k < 4; ++k) {
+            const uint64_t e = multi[back_window(data[k], left[k]) >> shift];
+            const unsigned count = multi_tokens(e);
+            store32(out[k], static_cast<uint32_t>(e));
+            out[k] += count;
+            rem[k] -= count;
+            left[k] -= multi_bits(e);
+        }
+    }
+    for (int k = 0; k < 4; ++k) {
+        for (; rem[k]; --rem[k]) {
+            const uint16_t e = t.decode[back_window(data[k], left[k]) >> shift];
+            *out[k]++ = static_cast<uint8_t>(e >> 8);
+            left[k] -= e & 0xFF;
+        }
+        if (left[k] != 0) fail(kCorruptStream, "Huff0 stream not fully consumed.");
     }
 }
 
@@ -688,12 +708,23 @@ size_t nzm1_encode(const Codebook& book, const uint8_t* src, size_t n, uint8_t* 
     return cursor;
 }
 
+static inline uint64_t load_be64(const uint8_t* p) {
+    uint64_t v;
+    std::memcpy(&v, p, 8);
+    return __builtin_bswap64(v);
+}
+
+// Lanes in order, one check per condition of mixed_huffman.h:180-240, with
+// its messages: per lane exactly `tokens` tokens over exactly `bits` bits,
+// zero padding, and the whole frame consumed. Whole tokens come from the
+// multi-token table where they fit the lane's counts; anything else (codes
+// over 12 bits, a lane's last tokens, a frame that runs short) takes one
+// token at a time.
 void nzm1_decode(const Codebook& book, const uint8_t* src, size_t size, uint8_t* dst, size_t n) {
-    // mixed_huffman.h:180-240: per lane exactly `tokens` tokens over exactly
-    // `bits` bits, zero padding, and the whole frame consumed
     if (size < 32) fail(kCorruptStream, "Truncated mixed Huffman frame.");
     size_t cursor = 32, written = 0;
-    std::vector<uint8_t> lane_buf;
+    thread_local std::vector<uint8_t> lane_buf;
+    const uint64_t* multi = book.multi.data();
     for (unsigned lane = 0; lane < 4; ++lane) {
         uint32_t tokens = 0, bits = 0;
         for (int b = 0; b < 4; ++b) {
@@ -702,15 +733,22 @@ void nzm1_decode(const Codebook& book, const uint8_t* src, size_t size, uint8_t*
         }
         const size_t bytes = (uint64_t(bits) + 7) / 8;
         if (bytes > size - cursor || tokens > n - written) fail(kCorruptStream, "Mixed frame lengths exceed its payload.");
+        // the lane, then zeros: an 8-byte read at any bit position below `bits` stays inside
         lane_buf.assign(src + cursor, src + cursor + bytes);
         lane_buf.resize(bytes + 16, 0);
+        const uint8_t* lane_bits = lane_buf.data();
         uint64_t pos = 0;
-        for (uint32_t t = 0; t < tokens; ++t) {
+        for (uint32_t left = tokens; left;) {
+            const uint64_t window = load_be64(lane_bits + (pos >> 3)) << (pos & 7);   // >= 57 valid bits
+            const uint64_t e = multi[window >> (64 - NZ_LUT_BITS)];
+            if (e && multi_tokens(e) <= left && pos + multi_bits(e) <= bits && n - written >= 4) {
+                store32(dst + written, static_cast<uint32_t>(e));
+                written += multi_bytes(e);
+                pos += multi_bits(e);
+                left -= multi_tokens(e);
+                continue;
+            }
             if (pos >= bits) fail(kCorruptStream, "Truncated mixed Huffman code.");
-            const uint8_t* p = lane_buf.data() + (pos >> 3);
-            uint64_t window = 0;
-            for (int b = 0; b < 8; ++b) window = (window << 8) | p[b];
-            if (pos & 7) window = (window << (pos & 7)) | (p[8] >> (8 - (pos & 7)));
             uint32_t value;
             unsigned count;
             const unsigned len = token_step(book, window, &value, &count);
@@ -718,6 +756,7 @@ void nzm1_decode(const Codebook& book, const uint8_t* src, size_t size, uint8_t*
             if (count > n - written) fail(kCorruptStream, "Mixed expansion exceeds exponent count.");
             for (unsigned b = 0; b < count; ++b) dst[written++] = static_cast<uint8_t>(value >> (8 * b));
             pos += len;
+            --left;
         }
         if (pos != bits) fail(kCorruptStream, "Mixed frame has unconsumed code bits.");
         if (bits % 8 && (src[cursor + bytes - 1] & ((1u << (8 - bits % 8)) - 1)))

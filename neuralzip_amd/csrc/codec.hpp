@@ -18,6 +18,7 @@ struct Huff0Tables {
     std::array<uint16_t, 256> codes{};
     unsigned log = 0;
     std::vector<uint16_t> decode;       // symbol << 8 | length, 1 << log entries
+    std::vector<uint64_t> multi;        // log-bit prefix -> whole symbols (multi_token_table)
 };
 
 Huff0Tables huff0_tables(const std::array<uint8_t, 256>& lengths);

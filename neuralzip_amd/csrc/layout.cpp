@@ -14,12 +14,6 @@
 namespace nz {
 namespace {
 
-uint32_t load_word(const uint8_t* p, unsigned es) {
-    uint32_t v = 0;
-    for (unsigned k = 0; k < es; ++k) v |= static_cast<uint32_t>(p[k]) << (8 * k);
-    return v;
-}
-
 // neuralzip/dtypes.py:23-45; only the byte-aligned exponent layouts reorder.
 uint32_t reorder_forward(uint32_t v, unsigned m, unsigned e) {
     return (v & ((1u << m) - 1u)) | ((v >> e) & (1u << m)) | ((v << 1) & (((1u << e) - 1u) << (m + 1)));

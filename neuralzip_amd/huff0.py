@@ -74,6 +74,18 @@ def _addr(arr):
     return arr.ctypes.data if arr.size else None
 
 
+_new_bytearray = ctypes.pythonapi.PyByteArray_FromStringAndSize
+_new_bytearray.restype = ctypes.py_object
+_new_bytearray.argtypes = [ctypes.c_void_p, ctypes.c_ssize_t]
+
+
+def _uninitialized_bytearray(size):
+    """A bytearray of `size` bytes left unwritten (no zero fill): for outputs
+    the native decoder writes completely; the pages are first touched by its
+    worker threads."""
+    return _new_bytearray(None, size) if size else bytearray()
+
+
 def count_mixed_tokens(chunks, vocab):
     """Greedy pair/singleton counts, each chunk parsed separately (mixed_huffman.h:96-115)."""
     vocab = _array(bytes(vocab))
@@ -264,7 +276,9 @@ def decompress_mixed_streams_many(tensor_specs, *, threads=0):
                     raise ValueError("Compressed chunk needs a decode table.")
                 chunks.append(_StorageIn(_MODE_IDS[mode], 0, _addr(data), data.size, int(symbols),
                                          _book_pointer(table) if table is not None and mode != "raw" else None))
-        out = bytearray(int(numel) * int(width))
+        # every byte is written: nz_storage_decompress checks that each lane's
+        # chunks cover the tensor exactly before it decodes anything
+        out = _uninitialized_bytearray(int(numel) * int(width))
         view = np.frombuffer(out, dtype=np.uint8) if len(out) else np.zeros(1, np.uint8)
         chunk_array = (_StorageIn * max(len(chunks), 1))(*chunks)
         size_array = (ctypes.c_uint64 * len(sizes))(*sizes)
