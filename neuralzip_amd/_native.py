@@ -4,11 +4,14 @@ The library must be built in-tree (``python -m neuralzip_amd.build`` or
 ``__graft_entry__.build()``); importing the GPU path without it raises.
 """
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
 
-LIBRARY = Path(__file__).resolve().parent / "libneuralzip_hip.so"
+# NZ_NATIVE_LIBRARY names another build of the same library (the
+# host-sanitized one the CPU suite can run against); by default the in-tree one
+LIBRARY = Path(os.environ.get("NZ_NATIVE_LIBRARY") or Path(__file__).resolve().parent / "libneuralzip_hip.so")
 
 FRAG_DESC = np.dtype([("bits", "<u8"), ("meta", "<u8"), ("lanes", "<u8"), ("out", "<u8"), ("lut", "<u8"),
                       ("bit_length", "<u8"), ("numel", "<u4"), ("lane_stride", "<u4"), ("kind", "<u4"),
@@ -45,6 +48,14 @@ class NativeError(RuntimeError):
     def __init__(self, code, message):
         super().__init__(message)
         self.code = code
+
+
+class NativeDataError(NativeError, ValueError):
+    """An invalid argument or a corrupt stream: a ValueError, as the
+    reference's decoders raise for bad data (decode_queue.h:29-109)."""
+
+
+_DATA_ERRORS = (-1, -5)   # NZ_INVALID_ARGUMENT, NZ_CORRUPT_STREAM
 
 
 class _FragmentSpec(ctypes.Structure):
@@ -129,7 +140,7 @@ def lib():
 
 def check(rc):
     if rc != 0:
-        raise NativeError(rc, lib().nz_last_error().decode())
+        raise (NativeDataError if rc in _DATA_ERRORS else NativeError)(rc, lib().nz_last_error().decode())
     return rc
 
 

@@ -616,22 +616,25 @@ static inline void store32(uint8_t* p, uint32_t v) { std::memcpy(p, &v, 4); }
 void huff0_decode4x(const Huff0Tables& t, const uint8_t* src, size_t size, uint8_t* dst, size_t n) {
     // HUF_decompress4X semantics: four streams of (n + 3) / 4 symbols (the
     // last takes the rest), each read backwards from its end mark, and each
-    // must end exactly at its first bit
+    // must end exactly at its first bit; Zstd reports every violation as
+    // "Data corruption detected", which the messages begin with
     if (n == 0) return;
-    if (size < 10 || n < 6) fail(kCorruptStream, "Huff0 4X block too small.");
+    if (size < 10 || n < 6) fail(kCorruptStream, "Data corruption detected: Huff0 4X block too small.");
     size_t lens[4];
     for (int k = 0; k < 3; ++k) lens[k] = src[2 * k] | (size_t(src[2 * k + 1]) << 8);
-    if (6 + lens[0] + lens[1] + lens[2] > size) fail(kCorruptStream, "Huff0 jump table exceeds its block.");
+    if (6 + lens[0] + lens[1] + lens[2] > size)
+        fail(kCorruptStream, "Data corruption detected: Huff0 jump table exceeds its block.");
     lens[3] = size - 6 - lens[0] - lens[1] - lens[2];
     const size_t segment = (n + 3) / 4;
-    if (3 * segment > n) fail(kCorruptStream, "Huff0 4X block too small.");
+    if (3 * segment > n) fail(kCorruptStream, "Data corruption detected: Huff0 4X block too small.");
     const uint8_t* data[4];
     int64_t left[4];
     uint8_t* out[4];
     size_t rem[4];
     const uint8_t* stream = src + 6;
     for (int k = 0; k < 4; ++k) {
-        if (!lens[k] || !stream[lens[k] - 1]) fail(kCorruptStream, "Backward bitstream lacks its end mark.");
+        if (!lens[k] || !stream[lens[k] - 1])
+            fail(kCorruptStream, "Data corruption detected: Backward bitstream lacks its end mark.");
         data[k] = stream;
         left[k] = static_cast<int64_t>(lens[k]) * 8 - (8 - highbit(stream[lens[k] - 1]));
         out[k] = dst + segment * k;
@@ -657,7 +660,7 @@ void huff0_decode4x(const Huff0Tables& t, const uint8_t* src, size_t size, uint8
             *out[k]++ = static_cast<uint8_t>(e >> 8);
             left[k] -= e & 0xFF;
         }
-        if (left[k] != 0) fail(kCorruptStream, "Huff0 stream not fully consumed.");
+        if (left[k] != 0) fail(kCorruptStream, "Data corruption detected: Huff0 stream not fully consumed.");
     }
 }
 
