@@ -256,12 +256,14 @@ def time_generate(model, ids, new_tokens):
     return full - first, out
 
 
-def graph_generate(model, ids, new_tokens, runtime=None):
+def graph_generate(model, ids, new_tokens, runtime=None, segmented=False):
     """Greedy decoding with a static KV cache whose steps are replayed from
     one HIP graph: the prompt and the first two steps run eagerly, the graph
     captures one step (with the runtime attached, its decode launches and
     side-stream prefetches included) and the remaining new_tokens - 3 steps
-    are replays. Returns (seconds of the replayed steps, their count, the
+    are replays. With `segmented`, the runtime's SegmentedGraph captures the
+    step instead (one graph per decode unit, decodes launched by the host
+    between them). Returns (seconds of the replayed steps, their count, the
     generated ids (batch, new_tokens))."""
     from transformers import StaticCache
     device = ids.device
@@ -288,10 +290,15 @@ def graph_generate(model, ids, new_tokens, runtime=None):
                 position += 1
         torch.cuda.current_stream(device).wait_stream(side)
         torch.cuda.synchronize(device)
-        graph = torch.cuda.CUDAGraph()
-        capture = runtime.graph_capture() if runtime is not None else contextlib.nullcontext()
-        with capture, torch.cuda.graph(graph):
-            out = step()
+        if segmented:
+            graph = runtime.segmented_graph()
+            with graph.capture():
+                out = step()
+        else:
+            graph = torch.cuda.CUDAGraph()
+            capture = runtime.graph_capture() if runtime is not None else contextlib.nullcontext()
+            with capture, torch.cuda.graph(graph):
+                out = step()
         torch.cuda.synchronize(device)
         replays = new_tokens - 3
         # a spin kernel on each side of the replays marks them in kernel traces
@@ -314,7 +321,7 @@ def graph_generate(model, ids, new_tokens, runtime=None):
 
 
 def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=None, new_tokens=None, graph=True,
-              fused_graph=False):
+              fused_graph=False, workspace_slots=None):
     """Greedy generation on a model shape of MODELS, uncompressed and with the
     NeuralZip runtime attached, on one GPU: eager Transformers generation
     (the reference's protocol: host-bound at small batches) and, with
@@ -355,7 +362,8 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
     log(f"setup: {len(setup.codebooks)} codebooks in {setup_s:.1f}s")
     t0 = time.perf_counter()
     exported = export_model_for_gpu(model, setup)
-    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=matvec, decode_slots=slots)
+    runtime = NeuralZipRuntime.attach(model, exported, device=device, matvec_tokens=matvec, decode_slots=slots,
+                                      workspace_slots=workspace_slots)
     attach_s = time.perf_counter() - t0
     log(f"export + attach: {len(exported.groups)} fragments, {len(exported.block_order)} blocks in {attach_s:.1f}s")
     with torch.no_grad():
@@ -384,6 +392,9 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
     nz_graph = graph_generate(model, ids, new_tokens, runtime) if graph else None
     if nz_graph:
         log(f"neuralzip graph: {nz_graph[0] / nz_graph[1] * 1e3:.3f} ms per replayed step")
+    nz_segmented = graph_generate(model, ids, new_tokens, runtime, segmented=True) if graph and not matvec else None
+    if nz_segmented:
+        log(f"neuralzip segmented graphs: {nz_segmented[0] / nz_segmented[1] * 1e3:.3f} ms per replayed step")
     matvec_info = {}
     if runtime._matvec:
         # one pass of fused products over every compressed Linear (one
@@ -427,6 +438,16 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                       "tokens_identical_to_uncompressed": bool(torch.equal(nz_graph[2].cpu(), base_graph[2].cpu())),
                       "uncompressed_graph_tokens_identical_to_eager": bool(torch.equal(base_graph[2].cpu(),
                                                                     base_out[:, prompt:].cpu()))}
+    segmented_info = None
+    if nz_segmented:
+        s_ms = nz_segmented[0] / nz_segmented[1] * 1e3
+        b_ms = base_graph[0] / base_graph[1] * 1e3
+        segmented_info = {"neuralzip_ms_per_step": round(s_ms, 3), "uncompressed_ms_per_step": round(b_ms, 3),
+                          "ratio_vs_uncompressed": round(s_ms / b_ms, 3), "replayed_steps": nz_segmented[1],
+                          "tokens_identical_to_uncompressed": bool(torch.equal(nz_segmented[2].cpu(),
+                                                                               base_graph[2].cpu())),
+                          "what": "NeuralZipRuntime.segmented_graph(): one HIP graph per decode unit, each unit's "
+                                  "decode launched by the host on the side stream once its slot is free"}
     fused_info = None
     if fused_graph and graph and not matvec:
         # the same compressed weights with fused decode-matvec products for
@@ -468,10 +489,12 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                    "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
-                   "prefetch": runtime.prefetch, "decode_slots": slots or "3/4 of the CUs (prefetch) or one per CU", **matvec_info},
+                   "prefetch": runtime.prefetch, "decode_slots": slots or "3/4 of the CUs (prefetch) or one per CU",
+                   "workspace_slots": len(set(runtime.block_slot.values())), **matvec_info},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "graph": graph_info,
+        "graph_segmented": segmented_info,
         "graph_fused": fused_info,
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
         "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
@@ -486,11 +509,13 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
 
 def model_benchmark(args):
     line = run_model(args.model, args.batch, args.dtype, args.matvec, args.slots, args.prompt, args.new_tokens,
-                     graph=not args.no_graph)
+                     graph=not args.no_graph, workspace_slots=args.workspace_slots)
     print(json.dumps(line), flush=True)
     exact = line["logits_bitwise_equal"] and (line["tokens_identical"] or args.matvec)
     if line["graph"] and not args.matvec:
         exact = exact and line["graph"]["tokens_identical_to_uncompressed"]
+    if line["graph_segmented"]:
+        exact = exact and line["graph_segmented"]["tokens_identical_to_uncompressed"]
     # fused products are not bit-identical to the GEMM, so generated tokens may differ there
     return 0 if exact else 1
 
@@ -502,6 +527,7 @@ def model_summary(line):
                       "ratio_vs_uncompressed": line["ratio_vs_uncompressed"],
                       "ms_per_step": line["ms_per_step"]},
             "graph": line["graph"],
+            "graph_segmented": line["graph_segmented"],
             "graph_fused": line["graph_fused"],
             "full_decode_pass_ms": line["config"]["full_decode_pass_ms"],
             "full_decode_pass_gbps": line["config"]["full_decode_pass_gbps"],
@@ -538,6 +564,43 @@ def trace_summary(path, kernel="nz_decode_kernel<2, true, false, false>", steps=
     return 0
 
 
+def trace_windows(path, steps):
+    """Per-step device time of the replay loops in a rocprofv3 kernel trace
+    (CSV) of a model run: graph_generate marks each loop with a spin kernel
+    before and after it. For each marked window: its length, the union of
+    kernel intervals (busy), the gaps, and kernel time summed by kind (GEMM,
+    decode, fused product, other), each divided by `steps` replays. Prints
+    JSON, one object per window in trace order."""
+    import csv
+    rows = []
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            rows.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]), row["Kernel_Name"]))
+    rows.sort()
+    marks = [i for i, (_, _, name) in enumerate(rows) if "spin_kernel" in name]
+    out = []
+    for a, b in zip(marks[0::2], marks[1::2]):
+        inside = rows[a + 1:b]
+        start, end = rows[a][1], rows[b][0]
+        busy, cursor = 0, start
+        for s, e, _ in inside:
+            s, e = max(s, cursor), min(e, end)
+            if e > s:
+                busy += e - s
+                cursor = e
+        kinds = {"gemm": 0, "decode": 0, "matvec": 0, "other": 0}
+        for s, e, name in inside:
+            kind = ("gemm" if name.startswith("Cijk") else "decode" if "nz_decode_kernel" in name
+                    else "matvec" if "nz_matvec" in name else "other")
+            kinds[kind] += e - s
+        per = 1e6 * steps
+        out.append({"kernels_per_step": round(len(inside) / steps, 1), "window_ms": round((end - start) / per, 3),
+                    "busy_ms": round(busy / per, 3), "gaps_ms": round((end - start - busy) / per, 3),
+                    **{f"{k}_ms": round(v / per, 3) for k, v in kinds.items()}})
+    print(json.dumps(out, indent=1), flush=True)
+    return 0
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -560,12 +623,19 @@ def main():
     parser.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the model's)")
     parser.add_argument("--new-tokens", type=int, default=None, help="generated tokens (default: the model's)")
     parser.add_argument("--no-graph", action="store_true", help="model benchmark: eager generation only")
+    parser.add_argument("--workspace-slots", type=int, default=None,
+                        help="model benchmark: workspace slots the decoded blocks take in turn (default 2)")
     parser.add_argument("--no-model", action="store_true",
                         help="default run: leave out the Llama-3-8B-shape bs=1 tok/s part of the line")
     parser.add_argument("--trace-summary", default=None, metavar="KERNEL_TRACE_CSV",
                         help="summarize a rocprofv3 kernel trace of a default run: the decode kernel's last "
                              "--steps dispatches (the timed steps)")
+    parser.add_argument("--trace-windows", default=None, metavar="KERNEL_TRACE_CSV",
+                        help="per-step device time of the marked replay loops of a model run's kernel trace "
+                             "(--steps: replays per loop)")
     args = parser.parse_args()
+    if args.trace_windows:
+        return trace_windows(args.trace_windows, args.steps)
     if args.trace_summary:
         return trace_summary(args.trace_summary, steps=args.steps)
     if args.copy_calibration:
@@ -733,7 +803,9 @@ def main():
     }
     print(json.dumps(line), flush=True)
     if model is not None and not (model["logits_bitwise_equal"] and model["tokens_identical"]
-                                  and (model["graph"] is None or model["graph"]["tokens_identical_to_uncompressed"])):
+                                  and (model["graph"] is None or model["graph"]["tokens_identical_to_uncompressed"])
+                                  and (model["graph_segmented"] is None
+                                       or model["graph_segmented"]["tokens_identical_to_uncompressed"])):
         return 1
     return 0
 

@@ -428,7 +428,7 @@ class NeuralZipRuntime:
     """
 
     def __init__(self, model, exported, device, *, prefetch=True, matvec_tokens=0, decode_slots=None,
-                 granularity="block", _store=None):
+                 granularity="block", workspace_slots=None, _store=None):
         if granularity not in GRANULARITIES:
             raise ValueError(f"granularity must be one of {GRANULARITIES}.")
         if granularity == "linear" and matvec_tokens:
@@ -461,10 +461,22 @@ class NeuralZipRuntime:
         self.units = order
         # unit -> the unit whose decode its hook prefetches (the first after the last)
         self._following = {name: order[(i + 1) % len(order)] for i, name in enumerate(order)}
-        n_slots = 1 if not self.prefetch or len(order) < 2 else (2 if len(order) % 2 == 0 else 3)
-        self.block_slot = {name: (i % 2 if n_slots > 1 else 0) for i, name in enumerate(order)}
-        if n_slots == 3:
-            self.block_slot[order[-1]] = 2
+        # Units take slots in turn (unit i: slot i mod `cycle`, where `cycle`
+        # = workspace_slots, default 2); when the last unit would share the
+        # first one's slot, which the last unit's hook prefetches into for the
+        # next forward, it gets a slot of its own.
+        if workspace_slots is not None and int(workspace_slots) < 2:
+            raise ValueError("workspace_slots must be at least 2.")
+        self.workspace_slots = None if workspace_slots is None else int(workspace_slots)
+        cycle = self.workspace_slots or 2
+        if not self.prefetch or len(order) < 2:
+            self.block_slot = {name: 0 for name in order}
+        else:
+            cycle = min(cycle, len(order))
+            self.block_slot = {name: i % cycle for i, name in enumerate(order)}
+            if (len(order) - 1) % cycle == 0:
+                self.block_slot[order[-1]] = cycle
+        n_slots = max(self.block_slot.values(), default=0) + 1
         unit_sizes = defaultdict(int)
         for unit, inner, layout, ids, config, binding in entries:
             key = (config.torch_dtype, self.block_slot[unit])
@@ -537,6 +549,8 @@ class NeuralZipRuntime:
         self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
         self._side_off = False  # graph_capture() decodes on the compute stream only
         self._captured = False  # graph_capture() was used: graphs may hold this runtime's buffers
+        self._segmenting = None  # the SegmentedGraph whose capture is in progress
+        self._eager_decodes = False  # hooks decoded since the last segmented replay
         self._matvec, self._matvec_blocks, self._partials = {}, frozenset(), None
         self._fused = set()    # blocks whose current call runs the fused products
         if self.matvec_tokens:
@@ -652,7 +666,7 @@ class NeuralZipRuntime:
 
     @classmethod
     def attach(cls, model, exported, *, device=None, prefetch=True, matvec_tokens=0, decode_slots=None,
-               granularity="block"):
+               granularity="block", workspace_slots=None):
         if hasattr(model, RUNTIME_ATTRIBUTE):
             raise RuntimeError("This model already has a NeuralZip runtime.")
         if not exported.groups:
@@ -676,7 +690,7 @@ class NeuralZipRuntime:
             module.__dict__.pop("weight", None)
         model.to(device).eval()
         runtime = cls(model, exported, device, prefetch=prefetch, matvec_tokens=matvec_tokens,
-                      decode_slots=decode_slots, granularity=granularity)
+                      decode_slots=decode_slots, granularity=granularity, workspace_slots=workspace_slots)
         runtime._grad_flags = grad_flags
         runtime._install()
         return runtime
@@ -747,6 +761,10 @@ class NeuralZipRuntime:
         return nn.functional.linear(input, module.weight, module.bias)
 
     def _decode_block(self, block_name, _module=None, _args=(), _kwargs=None):
+        if self._segmenting is not None:   # a segmented capture: a new graph starts here, nothing is decoded
+            self._segmenting._split(block_name)
+            return
+        self._eager_decodes = True
         stream = _current_stream_handle(self.device)
         if block_name in self._matvec_blocks:
             rows = self._token_rows(_args, _kwargs)
@@ -814,14 +832,16 @@ class NeuralZipRuntime:
         if getattr(self.model, RUNTIME_ATTRIBUTE, None) is self:
             delattr(self.model, RUNTIME_ATTRIBUTE)
         settings = dict(prefetch=self.prefetch or self.granularity != "block", matvec_tokens=self.matvec_tokens,
-                        decode_slots=self.decode_slots, granularity=self.granularity)
+                        decode_slots=self.decode_slots, granularity=self.granularity,
+                        workspace_slots=self.workspace_slots)
         settings.update(options)
         # The compressed store depends only on the decode units and their
         # slots. The new runtime takes it over when those stay; otherwise this
         # runtime's device buffers go first, so that two copies of the
         # compressed weights never coexist.
         same = (settings["granularity"] == self.granularity
-                and (bool(settings["prefetch"]) and settings["granularity"] == "block") == self.prefetch)
+                and (bool(settings["prefetch"]) and settings["granularity"] == "block") == self.prefetch
+                and settings["workspace_slots"] == self.workspace_slots)
         store = (self._store_key, self.store) if same else None
         self.store, self._prepared_batches, self._schedule_args = None, defaultdict(list), {}
         self._matvec, self._group_plans, self._outputs, self._partials = {}, {}, {}, None
@@ -856,6 +876,12 @@ class NeuralZipRuntime:
             self.drain()
             self._side_off = False
 
+    def segmented_graph(self):
+        """A SegmentedGraph of this runtime: one forward captured as one HIP
+        graph per decode unit, replayed with the units' decodes launched from
+        the host (see SegmentedGraph)."""
+        return SegmentedGraph(self)
+
     @torch.no_grad()
     def materialized_weights(self):
         """Yield compressed weights as bit-exact CPU tensors, one decode unit at a time."""
@@ -870,3 +896,118 @@ class NeuralZipRuntime:
                     continue
                 yielded.add(binding.tensor_name)
                 yield binding.tensor_name, self._binding_view(dtype, unit, binding).detach().to("cpu", copy=True)
+
+
+class SegmentedGraph:
+    """One forward captured as one HIP graph per decode unit, for replays
+    whose decodes overlap the compute stream without a second stream inside
+    any graph (no counterpart in the reference).
+
+    Capture (`with seg.capture(): out = forward()`): every unit's hook ends
+    the graph being captured and starts the next one, so the forward becomes
+    [prefix][unit 0][unit 1]..., all graphs sharing one memory pool; no
+    decode is captured. Replay (`seg.replay()`, on the current stream), for
+    each unit's graph in order: the host waits until the last earlier graph
+    (cyclically, so across replays too) that read the unit's workspace slot
+    has finished, launches the unit's decode on the side stream and records
+    `ready` there, the compute stream waits for `ready`, then the graph runs
+    and records `done`. The side stream therefore never holds a wait on the
+    compute stream: a pending cross-queue wait slows the compute stream's
+    dispatch of small kernels, and so does any second stream inside one
+    replayed graph. The host runs at most two units ahead of the device.
+
+    Replays must run in capture order (the graphs share a pool) and not
+    overlap another replay of this object. Eager forwards between replays
+    are allowed; a replay after them first waits for the device to finish
+    them. Writes to the workspaces from outside the runtime must have
+    finished before a replay (its decodes run on the side stream). Outputs
+    of the capture are rewritten by every replay.
+    """
+
+    def __init__(self, runtime):
+        if not runtime.prefetch or runtime.granularity != "block" or runtime._matvec:
+            raise ValueError("A segmented graph needs the block runtime with prefetch and without fused products.")
+        self.runtime = runtime
+        self.segments = []       # (unit or None, torch.cuda.CUDAGraph), in capture order
+        self._pool = None
+        self._open = None
+
+    @contextlib.contextmanager
+    def capture(self):
+        runtime = self.runtime
+        if self.segments or runtime._segmenting is not None:
+            raise RuntimeError("A segmented graph is captured once, one at a time.")
+        runtime.drain()
+        torch.cuda.synchronize(runtime.device)
+        runtime._captured = True
+        runtime._wrap = False   # replays rewrite the slots: eager forwards decode their first block themselves
+        stream = torch.cuda.Stream(runtime.device)
+        stream.wait_stream(torch.cuda.current_stream(runtime.device))
+        self._pool = torch.cuda.graph_pool_handle()
+        with torch.cuda.device(runtime.device), torch.cuda.stream(stream):
+            self._begin(None)
+            runtime._segmenting = self
+            try:
+                yield self
+            finally:
+                runtime._segmenting = None
+                self._end()
+        torch.cuda.current_stream(runtime.device).wait_stream(stream)
+        self._plan()
+
+    def _begin(self, unit):
+        graph = torch.cuda.CUDAGraph()
+        graph.capture_begin(pool=self._pool)
+        self._open = (unit, graph)
+
+    def _end(self):
+        unit, graph = self._open
+        self._open = None
+        graph.capture_end()
+        self.segments.append((unit, graph))
+
+    def _split(self, unit):
+        self._end()
+        self._begin(unit)
+
+    def _plan(self):
+        runtime = self.runtime
+        units = [unit for unit, _ in self.segments]
+        n = len(units)
+        # the last earlier segment, cyclically, whose unit uses the same slot
+        self._previous = []
+        for i, unit in enumerate(units):
+            previous = None
+            if unit is not None:
+                for back in range(1, n + 1):
+                    j = (i - back) % n
+                    if units[j] is not None and runtime.block_slot[units[j]] == runtime.block_slot[unit]:
+                        previous = j
+                        break
+            self._previous.append(previous)
+        with torch.cuda.device(runtime.device):
+            self._ready = [torch.cuda.Event() if unit is not None else None for unit in units]
+            self._done = [torch.cuda.Event() for _ in units]
+        self._launches = [runtime._schedule_args[unit] if unit is not None else None for unit in units]
+
+    def replay(self):
+        runtime = self.runtime
+        if not self.segments or self._open is not None:
+            raise RuntimeError("Capture the segmented graph before replaying it.")
+        if runtime._eager_decodes:
+            # eager forwards since the last replay may still read or write slots
+            runtime.drain()
+            torch.cuda.synchronize(runtime.device)
+            runtime._eager_decodes = False
+        compute = torch.cuda.current_stream(runtime.device)
+        side = runtime.side_stream
+        for i, (unit, graph) in enumerate(self.segments):
+            if unit is not None:
+                previous = self._previous[i]
+                if previous is not None:
+                    self._done[previous].synchronize()   # the slot's last reader has finished
+                _native.decode_schedule(self._launches[i], None, None, None, None, side.cuda_stream, None)
+                self._ready[i].record(side)
+                compute.wait_event(self._ready[i])
+            graph.replay()
+            self._done[i].record(compute)

@@ -285,3 +285,68 @@ def test_injected_weights_keep_the_original_gemm_path(granularity):
     assert "weight" not in model.layers[0]._parameters
     with torch.no_grad():
         assert exact(model.layers[0](x), expected)
+
+
+@pytest.mark.parametrize("n_blocks", [7, 8])
+def test_segmented_graph_replays_match_eager(n_blocks):
+    """runtime.segmented_graph(): one graph per block, decodes launched by the
+    host between them. Every replay gives the uncompressed model's bits,
+    with eager forwards on other inputs between replays, with the
+    workspaces poisoned before a replay, and with two and three slots
+    (even and odd block counts)."""
+    model, reference, named = _block_stack(n_blocks, seed=13)
+    setup = NeuralZipSetup(chunk_size=65536).build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
+    assert runtime.prefetch and len(set(runtime.block_slot.values())) == (2 if n_blocks % 2 == 0 else 3)
+    g = torch.Generator().manual_seed(6)
+    inputs = [torch.randn(4, 512, generator=g).to(torch.bfloat16).cuda() for _ in range(4)]
+    static = inputs[0].clone()
+    with torch.no_grad():
+        _run(model.blocks, static)   # warm-up before the capture
+        segmented = runtime.segmented_graph()
+        with segmented.capture():
+            out = _run(model.blocks, static)
+    assert [unit for unit, _ in segmented.segments] == [None] + [f"blocks.{i}" for i in range(n_blocks)]
+    with torch.no_grad():
+        for k, x in enumerate(inputs * 2):
+            static.copy_(x)
+            if k == 3:
+                torch.cuda.synchronize()
+                for workspace in runtime.workspaces.values():
+                    workspace.view(torch.uint8).fill_(0xFF)
+                torch.cuda.synchronize()   # writes from outside the runtime end before a replay
+            segmented.replay()
+            got = out.clone()
+            if k % 2:
+                eager = _run(model.blocks, inputs[(k + 1) % len(inputs)])   # eager work between replays
+                assert exact(eager, _run(reference.blocks, inputs[(k + 1) % len(inputs)])), f"eager after {k}"
+            torch.cuda.synchronize()
+            assert exact(got, _run(reference.blocks, x)), f"replay {k}"
+
+
+def test_segmented_graph_with_a_block_called_twice():
+    """A forward that calls one block twice and skips another: the captured
+    segments follow the calls, each decodes its block, and replays match."""
+    model, reference, named = _block_stack(5, seed=14)
+    setup = NeuralZipSetup(chunk_size=65536).build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
+    order = [0, 1, 1, 3, 2, 4]
+    x = torch.randn(4, 512, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).cuda()
+
+    def forward(blocks, h):
+        for i in order:
+            h = blocks[i](h)
+        return h
+    static = x.clone()
+    with torch.no_grad():
+        forward(model.blocks, static)
+        segmented = runtime.segmented_graph()
+        with segmented.capture():
+            out = forward(model.blocks, static)
+        expected = forward(reference.blocks, x)
+        for _ in range(3):
+            segmented.replay()
+            torch.cuda.synchronize()
+            assert exact(out, expected)
+    with pytest.raises(RuntimeError, match="graphs_released"):
+        runtime.replace(decode_slots=64)
