@@ -256,14 +256,12 @@ def time_generate(model, ids, new_tokens):
     return full - first, out
 
 
-def graph_generate(model, ids, new_tokens, runtime=None, segmented=False):
+def graph_generate(model, ids, new_tokens, runtime=None):
     """Greedy decoding with a static KV cache whose steps are replayed from
     one HIP graph: the prompt and the first two steps run eagerly, the graph
     captures one step (with the runtime attached, its decode launches and
     side-stream prefetches included) and the remaining new_tokens - 3 steps
-    are replays. With `segmented`, the runtime's SegmentedGraph captures the
-    step instead (one graph per decode unit, decodes launched by the host
-    between them). Returns (seconds of the replayed steps, their count, the
+    are replays. Returns (seconds of the replayed steps, their count, the
     generated ids (batch, new_tokens))."""
     from transformers import StaticCache
     device = ids.device
@@ -290,15 +288,10 @@ def graph_generate(model, ids, new_tokens, runtime=None, segmented=False):
                 position += 1
         torch.cuda.current_stream(device).wait_stream(side)
         torch.cuda.synchronize(device)
-        if segmented:
-            graph = runtime.segmented_graph()
-            with graph.capture():
-                out = step()
-        else:
-            graph = torch.cuda.CUDAGraph()
-            capture = runtime.graph_capture() if runtime is not None else contextlib.nullcontext()
-            with capture, torch.cuda.graph(graph):
-                out = step()
+        graph = torch.cuda.CUDAGraph()
+        capture = runtime.graph_capture() if runtime is not None else contextlib.nullcontext()
+        with capture, torch.cuda.graph(graph):
+            out = step()
         torch.cuda.synchronize(device)
         replays = new_tokens - 3
         # a spin kernel on each side of the replays marks them in kernel traces
@@ -392,9 +385,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
     nz_graph = graph_generate(model, ids, new_tokens, runtime) if graph else None
     if nz_graph:
         log(f"neuralzip graph: {nz_graph[0] / nz_graph[1] * 1e3:.3f} ms per replayed step")
-    nz_segmented = graph_generate(model, ids, new_tokens, runtime, segmented=True) if graph and not matvec else None
-    if nz_segmented:
-        log(f"neuralzip segmented graphs: {nz_segmented[0] / nz_segmented[1] * 1e3:.3f} ms per replayed step")
+
     matvec_info = {}
     if runtime._matvec:
         # one pass of fused products over every compressed Linear (one
@@ -438,16 +429,6 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                       "tokens_identical_to_uncompressed": bool(torch.equal(nz_graph[2].cpu(), base_graph[2].cpu())),
                       "uncompressed_graph_tokens_identical_to_eager": bool(torch.equal(base_graph[2].cpu(),
                                                                     base_out[:, prompt:].cpu()))}
-    segmented_info = None
-    if nz_segmented:
-        s_ms = nz_segmented[0] / nz_segmented[1] * 1e3
-        b_ms = base_graph[0] / base_graph[1] * 1e3
-        segmented_info = {"neuralzip_ms_per_step": round(s_ms, 3), "uncompressed_ms_per_step": round(b_ms, 3),
-                          "ratio_vs_uncompressed": round(s_ms / b_ms, 3), "replayed_steps": nz_segmented[1],
-                          "tokens_identical_to_uncompressed": bool(torch.equal(nz_segmented[2].cpu(),
-                                                                               base_graph[2].cpu())),
-                          "what": "NeuralZipRuntime.segmented_graph(): one HIP graph per decode unit, each unit's "
-                                  "decode launched by the host on the side stream once its slot is free"}
     fused_info = None
     if fused_graph and graph and not matvec:
         # the same compressed weights with fused decode-matvec products for
@@ -494,7 +475,6 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
         "graph": graph_info,
-        "graph_segmented": segmented_info,
         "graph_fused": fused_info,
         "logits_bitwise_equal": bool(torch.equal(logits.view(torch.int32), ref_logits.view(torch.int32))),
         "tokens_identical": bool(torch.equal(nz_out.cpu(), base_out.cpu())),
@@ -514,8 +494,6 @@ def model_benchmark(args):
     exact = line["logits_bitwise_equal"] and (line["tokens_identical"] or args.matvec)
     if line["graph"] and not args.matvec:
         exact = exact and line["graph"]["tokens_identical_to_uncompressed"]
-    if line["graph_segmented"]:
-        exact = exact and line["graph_segmented"]["tokens_identical_to_uncompressed"]
     # fused products are not bit-identical to the GEMM, so generated tokens may differ there
     return 0 if exact else 1
 
@@ -527,7 +505,6 @@ def model_summary(line):
                       "ratio_vs_uncompressed": line["ratio_vs_uncompressed"],
                       "ms_per_step": line["ms_per_step"]},
             "graph": line["graph"],
-            "graph_segmented": line["graph_segmented"],
             "graph_fused": line["graph_fused"],
             "full_decode_pass_ms": line["config"]["full_decode_pass_ms"],
             "full_decode_pass_gbps": line["config"]["full_decode_pass_gbps"],
@@ -803,9 +780,7 @@ def main():
     }
     print(json.dumps(line), flush=True)
     if model is not None and not (model["logits_bitwise_equal"] and model["tokens_identical"]
-                                  and (model["graph"] is None or model["graph"]["tokens_identical_to_uncompressed"])
-                                  and (model["graph_segmented"] is None
-                                       or model["graph_segmented"]["tokens_identical_to_uncompressed"])):
+                                  and (model["graph"] is None or model["graph"]["tokens_identical_to_uncompressed"])):
         return 1
     return 0
 

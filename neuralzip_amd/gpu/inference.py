@@ -911,7 +911,8 @@ class SegmentedGraph:
     (cyclically, so across replays too) that read the unit's workspace slot
     has finished, launches the unit's decode on the side stream and records
     `ready` there, the compute stream waits for `ready`, then the graph runs
-    and records `done`. The side stream therefore never holds a wait on the
+    and records `done` (the graph before the first unit waits on the side
+    stream too, so every graph of a replay starts behind a wait). The side stream therefore never holds a wait on the
     compute stream: a pending cross-queue wait slows the compute stream's
     dispatch of small kernels, and so does any second stream inside one
     replayed graph. The host runs at most two units ahead of the device.
@@ -924,7 +925,16 @@ class SegmentedGraph:
     of the capture are rewritten by every replay.
     """
 
+    # Switched off: replays of these graphs with the decode launches left
+    # out (timing probes) ended in a queue abort on the device, reported in
+    # a KV-cache index_copy kernel, whose cause is not known; the replay
+    # below has not failed, but shares their structure.
+    ENABLED = False
+
     def __init__(self, runtime):
+        if not self.ENABLED:
+            raise RuntimeError("Segmented graph replay is switched off: related replays failed on the device "
+                               "for a reason not yet known.")
         if not runtime.prefetch or runtime.granularity != "block" or runtime._matvec:
             raise ValueError("A segmented graph needs the block runtime with prefetch and without fused products.")
         self.runtime = runtime
@@ -986,7 +996,7 @@ class SegmentedGraph:
                         break
             self._previous.append(previous)
         with torch.cuda.device(runtime.device):
-            self._ready = [torch.cuda.Event() if unit is not None else None for unit in units]
+            self._ready = [torch.cuda.Event() for _ in units]
             self._done = [torch.cuda.Event() for _ in units]
         self._launches = [runtime._schedule_args[unit] if unit is not None else None for unit in units]
 
@@ -1007,7 +1017,9 @@ class SegmentedGraph:
                 if previous is not None:
                     self._done[previous].synchronize()   # the slot's last reader has finished
                 _native.decode_schedule(self._launches[i], None, None, None, None, side.cuda_stream, None)
-                self._ready[i].record(side)
-                compute.wait_event(self._ready[i])
+            # every graph starts behind a wait on the side stream (for a unit,
+            # its decode): no two graphs of a replay are launched back to back
+            self._ready[i].record(side)
+            compute.wait_event(self._ready[i])
             graph.replay()
             self._done[i].record(compute)

@@ -287,6 +287,11 @@ def test_injected_weights_keep_the_original_gemm_path(granularity):
         assert exact(model.layers[0](x), expected)
 
 
+SEGMENTED_OFF = pytest.mark.skip(reason="segmented graph replay is switched off: timing probes of the same graphs "
+                                        "with the decodes left out ended in a device queue abort of unknown cause")
+
+
+@SEGMENTED_OFF
 @pytest.mark.parametrize("n_blocks", [7, 8])
 def test_segmented_graph_replays_match_eager(n_blocks):
     """runtime.segmented_graph(): one graph per block, decodes launched by the
@@ -324,6 +329,7 @@ def test_segmented_graph_replays_match_eager(n_blocks):
             assert exact(got, _run(reference.blocks, x)), f"replay {k}"
 
 
+@SEGMENTED_OFF
 def test_segmented_graph_with_a_block_called_twice():
     """A forward that calls one block twice and skips another: the captured
     segments follow the calls, each decodes its block, and replays match."""
@@ -350,3 +356,11 @@ def test_segmented_graph_with_a_block_called_twice():
             assert exact(out, expected)
     with pytest.raises(RuntimeError, match="graphs_released"):
         runtime.replace(decode_slots=64)
+
+
+def test_segmented_graph_is_switched_off():
+    model, _, named = _block_stack(2, seed=15)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, NeuralZipSetup(chunk_size=65536).build(named)),
+                                      device="cuda:0")
+    with pytest.raises(RuntimeError, match="switched off"):
+        runtime.segmented_graph()
