@@ -31,20 +31,25 @@ class DTypeSpec:
         return self.exponent_stream if self.exponent_stream is not None else self.element_size - 1
 
     def reorder_bytes(self, raw_bytes, *, restore=False):
-        """Move the sign below the exponent, or undo it; layout 0 is identity."""
+        """The words with the sign bit moved from the top of the word to just
+        below the exponent field, or back with `restore` (dtypes.py:23-45).
+        A word of size S bits with M mantissa bits is sign:exponent:mantissa
+        from the top; reordered it is exponent:sign:mantissa, so the
+        exponent of a bfloat16 or float32 word fills its top byte. Layouts
+        without the reorder (float16) are returned as they are."""
         if not self.bit_reorder:
             return raw_bytes
-        unsigned = self.numpy.type
-        exponent_bits = self.exponent_mask.bit_length()
-        values = np.frombuffer(raw_bytes, dtype=self.numpy)
-        mantissa = values & unsigned((1 << self.mantissa_bits) - 1)
+        words = np.frombuffer(raw_bytes, dtype=self.numpy)
+        m = self.mantissa_bits
+        top = 8 * self.element_size - 1                       # the sign bit of the original word
+        fraction = words & self.numpy.type((1 << m) - 1)
         if restore:
-            sign = (values << unsigned(exponent_bits)) & unsigned(1 << (self.mantissa_bits + exponent_bits))
-            exponent = (values >> unsigned(1)) & unsigned(self.exponent_mask << self.mantissa_bits)
+            sign, exponent = (words >> m) & 1, words >> (m + 1)
+            out = (sign << top) | (exponent << m) | fraction
         else:
-            sign = (values >> unsigned(exponent_bits)) & unsigned(1 << self.mantissa_bits)
-            exponent = (values << unsigned(1)) & unsigned(self.exponent_mask << (self.mantissa_bits + 1))
-        return (sign | exponent | mantissa).astype(self.numpy, copy=False).tobytes()
+            sign, exponent = words >> top, (words >> m) & self.exponent_mask
+            out = (exponent << (m + 1)) | (sign << m) | fraction
+        return out.astype(self.numpy).tobytes()
 
     def selected_lane(self, raw_bytes):
         """The selected byte lane of the reordered words, without reordering

@@ -1,8 +1,14 @@
 """Storage format v2: one uint8 blob plus JSON metadata (neuralzip/storage.py).
 
-Blob layout (written by huff0.compress_direct_storage): codebook prefix
-(header then vocab for each codebook), the raw lanes of every tensor, then
-the compacted selected-lane payloads.
+Blob, front to back (written by huff0.compress_direct_storage):
+  * the codebook prefix: each codebook's header, then its pair vocabulary,
+    in the order of the metadata's codebook records;
+  * every tensor's lanes other than the selected one, lane after lane, one
+    byte per element each;
+  * the selected lane's chunk payloads of all tensors, in order, each raw
+    bytes or a coded block (Huff0 4X or NZM1).
+Metadata: {"version": 2, "codebooks": [...], "tensors": [...]}, every byte
+range an [offset, size] span into the blob.
 """
 import torch
 
@@ -32,6 +38,19 @@ def _pack_codebooks(codebooks):
     return prefix, records
 
 
+def _readonly_bytes(blob):
+    """A flat read-only byte view of a storage blob given as a tensor (on any
+    device), an array or a buffer; only a non-contiguous buffer is copied."""
+    if torch.is_tensor(blob):
+        blob = blob.detach().cpu().contiguous().reshape(-1).numpy()
+    view = memoryview(blob)
+    if view.nbytes == 0:
+        return memoryview(b"")
+    if not view.c_contiguous:
+        view = memoryview(view.tobytes())
+    return view.cast("B").toreadonly()
+
+
 def unpack_storage(blob, metadata):
     """Codebook and tensor payloads as read-only views into `blob`.
 
@@ -40,18 +59,13 @@ def unpack_storage(blob, metadata):
     """
     if int(metadata["version"]) != FORMAT_VERSION:
         raise ValueError("Unsupported NeuralZip storage checkpoint.")
-    if torch.is_tensor(blob):
-        blob = blob.detach().cpu().contiguous().numpy().reshape(-1)
-    view = memoryview(blob)
-    if not view.c_contiguous or not view.nbytes:
-        view = memoryview(view.tobytes())
-    view = view.cast("B").toreadonly()
+    data = _readonly_bytes(blob)
 
     def span(pair):
         offset, size = (int(v) for v in pair)
-        if offset < 0 or size < 0 or offset + size > len(view):
+        if min(offset, size) < 0 or offset + size > len(data):
             raise ValueError("A NeuralZip storage span is outside its data tensor.")
-        return view[offset:offset + size]
+        return data[offset:offset + size]
 
     codebooks = tuple(
         CodebookPayload(codebook_id=record["id"], stream_id=record["stream"], dtype=record["dtype"],
@@ -69,38 +83,44 @@ def unpack_storage(blob, metadata):
     return codebooks, tensors
 
 
+def _tensor_record(name, tensor, spec, lanes):
+    """A tensor's metadata record; `lanes` holds each lane's chunks as the
+    encoder reports them: (mode, symbols, codebook id or -1, offset, size)."""
+    return {
+        "name": str(name),
+        "shape": [int(d) for d in tensor.shape],
+        "dtype": spec.name,
+        "element_size": spec.element_size,
+        "numel": int(tensor.numel()),
+        "bit_reorder": int(spec.bit_reorder),
+        "groups": [[{"mode": str(mode), "symbols": int(symbols), "codebook": None if int(book) < 0 else int(book),
+                     "payload": [int(offset), int(size)]} for mode, symbols, book, offset, size in lane]
+                   for lane in lanes],
+    }
+
+
 def pack_direct_storage(named_tensors, specs, codebooks, prefix, codebook_metadata, packed, native_groups):
     """Blob tensor, metadata and size accounting from the native encoder's
-    spans; codebooks no chunk uses are dropped (storage.py:105-164)."""
-    used = {chunk[2] for groups in native_groups for group in groups for chunk in group}
-    kept = tuple(book for book in codebooks if book.codebook_id in used)
-    shift = 0
+    output: `packed` holds the codebook prefix written for `codebooks`, the
+    raw lanes and the payloads, `native_groups` the spans of every chunk
+    (storage.py:105-164). A codebook whose chunks all stayed raw is not
+    stored: the prefix is rewritten without it, and every span behind the
+    prefix moves back by the bytes the prefix lost."""
+    tensors = [_tensor_record(name, tensor, spec[1], lanes)
+               for (name, tensor), spec, lanes in zip(named_tensors, specs, native_groups, strict=True)]
+    coded = {chunk["codebook"] for record in tensors for lane in record["groups"] for chunk in lane}
+    kept = tuple(book for book in codebooks if book.codebook_id in coded)
     if len(kept) != len(codebooks):
-        new_prefix, codebook_metadata = _pack_codebooks(kept)
-        shift = len(prefix) - len(new_prefix)
-        packed[:len(prefix)] = new_prefix
-        codebooks = kept
-    tensors = []
-    for (name, tensor), spec, groups in zip(named_tensors, specs, native_groups, strict=True):
-        config = spec[1]
-        tensors.append({
-            "name": str(name),
-            "shape": [int(d) for d in tensor.shape],
-            "dtype": config.name,
-            "element_size": config.element_size,
-            "numel": int(tensor.numel()),
-            "bit_reorder": int(config.bit_reorder),
-            "groups": [[{"mode": str(mode), "symbols": int(symbols),
-                         "codebook": None if int(codebook_id) < 0 else int(codebook_id),
-                         "payload": [int(offset), int(size)]}
-                        for mode, symbols, codebook_id, offset, size in group] for group in groups],
-        })
-    if shift:
+        compact, codebook_metadata = _pack_codebooks(kept)
+        lost = len(prefix) - len(compact)
+        packed[:len(compact)] = compact
+        del packed[len(compact):len(prefix)]
         for record in tensors:
-            for group in record["groups"]:
-                for chunk in group:
+            for lane in record["groups"]:
+                for chunk in lane:
                     if chunk["payload"][0] >= len(prefix):
-                        chunk["payload"][0] -= shift
+                        chunk["payload"][0] -= lost
+        codebooks = kept
     blob = _bytes_tensor(packed)
     metadata = {"version": FORMAT_VERSION, "codebooks": codebook_metadata, "tensors": tensors}
     return blob, metadata, storage_bytes(codebooks, tensors, blob.numel())

@@ -129,3 +129,25 @@ def test_decompress_many_validates_alignment():
         oracle.decompress_many([(2, True, 1024, bad)])
     with pytest.raises(oracle.OracleError, match="numel"):
         oracle.decompress_many([(2, True, 1024, ((good,), (("raw", b"x" * 10, 10, None),)))])
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_product_reorder_matches_the_oracle_lane_split(dtype):
+    """The product's DTypeSpec.reorder_bytes, both ways, against the oracle's
+    lane split and restore: every 16-bit pattern, random and edge 32-bit
+    words (including NaNs, infinities, signed zeros and subnormals)."""
+    from neuralzip_amd.dtypes import DTYPES
+    spec = DTYPES[getattr(torch, dtype)]
+    es, reorder, m, e, _ = SPECS[getattr(torch, dtype)]
+    if es == 2:
+        words = np.arange(65536, dtype=np.uint16)
+    else:
+        rng = np.random.default_rng(9)
+        edges = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0xFFFFFFFF, 1, 0x807FFFFF], np.uint32)
+        words = np.concatenate([edges, rng.integers(0, 1 << 32, 1 << 16, dtype=np.uint32)])
+    raw = words.tobytes()
+    reordered = np.frombuffer(spec.reorder_bytes(raw), dtype=np.uint8)
+    lanes = oracle.split_lanes(raw, es, reorder, m, e)
+    for k in range(es):
+        assert np.array_equal(reordered[k::es], lanes[k]), k
+    assert spec.reorder_bytes(spec.reorder_bytes(raw), restore=True) == raw

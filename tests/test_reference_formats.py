@@ -344,15 +344,24 @@ def test_gpu_checkpoint_v3_fixture_attaches_bit_exactly(tmp_path, patched):
 
 
 @pytest.mark.gpu
-def test_gpu_decodes_archive_fixture_tensors():
+@pytest.mark.parametrize("which", ["bf16_fp16", "fp32"])
+def test_gpu_decodes_archive_fixture_tensors(which):
     """The fixture archive's coded tensors (Huff0 chunks written by libzstd,
-    NZM1 frames, raw chunks; bf16 and fp16) exported with the fixture's
-    setup and decoded by the HIP kernel, bit for bit."""
+    NZM1 frames, raw chunks; bf16, fp16 and fp32) exported with the
+    fixture's setup and decoded by the HIP kernel, bit for bit. The fp32
+    tensor's last chunk is planned with a codebook lacking its symbols,
+    which the GPU export refuses (as the reference's does): it is planned
+    raw here."""
     from neuralzip_amd.gpu import decoder as gpu_decoder
     from neuralzip_amd.dtypes import DTYPES
     from neuralzip_amd.gpu.inference import export_tensors_for_gpu
     setup = NeuralZipSetup.load(FIXTURES / "setup.pkl")
-    tensors = dict(expected_archive()[:3])
+    if which == "fp32":
+        key = ("t3.fp32", "float32", 3, 11000)
+        setup.chunk_codebooks[key] = setup.chunk_codebooks[key][:3] + (None,)
+        tensors = dict(expected_archive()[3:4])
+    else:
+        tensors = dict(expected_archive()[:3])
     exported = export_tensors_for_gpu(tensors, setup)
     assert {name for *_, name in exported.tensors} == set(tensors)
     device = torch.device("cuda:0")
