@@ -208,17 +208,24 @@ int nz_event_destroy(void* event);
 /* The stream work of one decode-hook call, in one call:
  *   1. if `wait` is not NULL, `stream` waits for it;
  *   2. the `n_inline` launches of `inline_launches` run on `stream`;
- *   3. if `n_ahead` > 0: `ready` is recorded on `stream`, `side` waits for
- *      it, the `n_ahead` launches of `ahead_launches` run on `side` (so they
- *      start after everything queued on `stream` so far) and `done` is
- *      recorded on `side`.
+ *   3. if `n_ahead` > 0: `ready` (if not NULL) is recorded on `stream`,
+ *      `side` waits for `after`, or for `ready` when `after` is NULL, the
+ *      `n_ahead` launches of `ahead_launches` run on `side` and `done` is
+ *      recorded on `side`. With `after` NULL the launches start after
+ *      everything queued on `stream` so far. An `after` recorded on `stream`
+ *      by an earlier call lets them start once the work queued before that
+ *      record has run; the caller guarantees that nothing queued since reads
+ *      what they overwrite. Waiting for an event that has already completed
+ *      costs the host well under a microsecond, for one just recorded about
+ *      20 (MI355X, ROCm 7.2).
  * Events come from nz_event_create. Replaces the stream and event calls of
  * the reference's pre-forward hook and of this runtime's side-stream
  * prefetch of block N+1 (neuralzip/gpu/inference.py:476-493), which cost a
- * Python-level call each. Works under HIP stream capture: the records and
- * waits become the graph's dependencies between the two streams. */
+ * Python-level call each. Works under HIP stream capture, with `after`
+ * recorded in the same capture: the records and waits become the graph's
+ * dependencies between the two streams. */
 int nz_decode_schedule(const nz_decode_args* inline_launches, uint32_t n_inline, const nz_decode_args* ahead_launches,
-                       uint32_t n_ahead, void* wait, void* ready, void* done, void* stream, void* side);
+                       uint32_t n_ahead, void* wait, void* ready, void* after, void* done, void* stream, void* side);
 
 /* CPU emulation of nz_decode_launch on host copies of the same arrays; a
  * test hook for GPU-less hosts, never used by the runtime. */

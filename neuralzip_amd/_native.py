@@ -119,7 +119,7 @@ def lib():
         L.nz_decode_launch_ex.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, u32, vp]
         L.nz_event_create.argtypes = [ctypes.POINTER(vp)]
         L.nz_event_destroy.argtypes = [vp]
-        L.nz_decode_schedule.argtypes = [vp, u32, vp, u32, vp, vp, vp, vp, vp]
+        L.nz_decode_schedule.argtypes = [vp, u32, vp, u32, vp, vp, vp, vp, vp, vp]
         L.nz_emulate_decode.argtypes = [vp, vp, vp, vp, u32, ctypes.c_int, ctypes.c_int, vp]
         L.nz_matvec_plan.argtypes = [vp, vp, u32, vp, u32, u32, ctypes.c_int, vp, vp, u32, ctypes.POINTER(u32)]
         L.nz_matvec_tiles.argtypes = [vp, u32, vp, u32, vp, u32, u32, ctypes.c_int, u64, vp]
@@ -315,10 +315,10 @@ def event_destroy(handle):
     check(lib().nz_event_destroy(handle))
 
 
-def decode_schedule(inline, ahead, wait, ready, done, stream, side):
+def decode_schedule(inline, ahead, wait, ready, done, stream, side, after=None):
     """nz_decode_schedule: `inline` and `ahead` are DecodeArgs arrays (or None)."""
     check(lib().nz_decode_schedule(inline, len(inline) if inline is not None else 0, ahead,
-                                   len(ahead) if ahead is not None else 0, wait, ready, done, stream, side))
+                                   len(ahead) if ahead is not None else 0, wait, ready, after, done, stream, side))
 
 
 def emulate_decode(base, descs, tiles, segments, element_size, bit_reorder, out):

@@ -262,8 +262,8 @@ int nz_event_destroy(void* event) {
 }
 
 int nz_decode_schedule(const nz_decode_args* inline_launches, uint32_t n_inline, const nz_decode_args* ahead_launches,
-                       uint32_t n_ahead, void* wait, void* ready, void* done, void* stream, void* side) {
-    if ((n_inline && !inline_launches) || (n_ahead && (!ahead_launches || !ready || !done)))
+                       uint32_t n_ahead, void* wait, void* ready, void* after, void* done, void* stream, void* side) {
+    if ((n_inline && !inline_launches) || (n_ahead && (!ahead_launches || !(ready || after) || !done)))
         return set_error(nz::kInvalidArgument, "Null decode schedule argument.");
     for (uint32_t i = 0; i < n_inline + n_ahead; ++i) {
         const nz_decode_args& a = i < n_inline ? inline_launches[i] : ahead_launches[i - n_inline];
@@ -279,8 +279,8 @@ int nz_decode_schedule(const nz_decode_args* inline_launches, uint32_t n_inline,
     for (uint32_t i = 0; i < n_inline; ++i)
         if ((rc = run(inline_launches[i], stream)) != 0) return rc;
     if (!n_ahead) return 0;
-    if ((rc = nz_hip_event_record(ready, stream, message, sizeof message)) != 0 ||
-        (rc = nz_hip_stream_wait(side, ready, message, sizeof message)) != 0)
+    if ((ready && (rc = nz_hip_event_record(ready, stream, message, sizeof message)) != 0) ||
+        (rc = nz_hip_stream_wait(side, after ? after : ready, message, sizeof message)) != 0)
         return set_error(rc, message);
     for (uint32_t i = 0; i < n_ahead; ++i)
         if ((rc = run(ahead_launches[i], side)) != 0) return rc;

@@ -40,6 +40,12 @@ GRANULARITIES = ("block", "linear")
 # blocks of at least this many decoded bytes on average and decodes smaller
 # ones on the compute stream.
 GRAPH_PREFETCH_MIN_BYTES = 64 << 20
+# Workspace slots that prefetching units take in turn. With three, the unit
+# that ran since the previous hook never holds the slot being refilled, so
+# the side stream can wait for that hook's record instead of one made in the
+# same call: about 20 us less host time per hook, and eager 8B batch-1 steps
+# 0.6 ms faster (MI355X, ROCm 7.2).
+DEFAULT_WORKSPACE_SLOTS = 3
 _GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
 # Tensor offsets in a workspace: 128 elements keeps views 256-byte aligned
 # and fragment starts 16-element aligned (the layout's vector alignment).
@@ -399,6 +405,20 @@ def _binding_module(model, binding):
     return module
 
 
+def _unit_slots(order, cycle):
+    """Workspace slot of each unit of `order`: unit i takes slot i mod
+    `cycle`; when the last unit would share the first one's slot, which the
+    last unit's hook prefetches into for the next forward, it gets a slot of
+    its own. `cycle` 1 (no prefetch) puts every unit in slot 0."""
+    if cycle < 2 or len(order) < 2:
+        return {name: 0 for name in order}
+    cycle = min(cycle, len(order))
+    slots = {name: i % cycle for i, name in enumerate(order)}
+    if (len(order) - 1) % cycle == 0:
+        slots[order[-1]] = cycle
+    return slots
+
+
 def _current_stream_handle(device):
     """The device's current HIP stream as an integer handle."""
     return torch._C._cuda_getCurrentRawStream(device.index)
@@ -461,21 +481,10 @@ class NeuralZipRuntime:
         self.units = order
         # unit -> the unit whose decode its hook prefetches (the first after the last)
         self._following = {name: order[(i + 1) % len(order)] for i, name in enumerate(order)}
-        # Units take slots in turn (unit i: slot i mod `cycle`, where `cycle`
-        # = workspace_slots, default 2); when the last unit would share the
-        # first one's slot, which the last unit's hook prefetches into for the
-        # next forward, it gets a slot of its own.
         if workspace_slots is not None and int(workspace_slots) < 2:
             raise ValueError("workspace_slots must be at least 2.")
         self.workspace_slots = None if workspace_slots is None else int(workspace_slots)
-        cycle = self.workspace_slots or 2
-        if not self.prefetch or len(order) < 2:
-            self.block_slot = {name: 0 for name in order}
-        else:
-            cycle = min(cycle, len(order))
-            self.block_slot = {name: i % cycle for i, name in enumerate(order)}
-            if (len(order) - 1) % cycle == 0:
-                self.block_slot[order[-1]] = cycle
+        self.block_slot = _unit_slots(order, (self.workspace_slots or DEFAULT_WORKSPACE_SLOTS) if self.prefetch else 1)
         n_slots = max(self.block_slot.values(), default=0) + 1
         unit_sizes = defaultdict(int)
         for unit, inner, layout, ids, config, binding in entries:
@@ -546,6 +555,7 @@ class NeuralZipRuntime:
                             if self.prefetch else {})
         weakref.finalize(self, _destroy_events, self.device, [e for pair in self._events.values() for e in pair])
         self._pending = None   # (unit name, event) decoded ahead on the side stream
+        self._marker = None    # (unit, event, stream): the last hook's record on the compute stream
         self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
         self._side_off = False  # graph_capture() decodes on the compute stream only
         self._captured = False  # graph_capture() was used: graphs may hold this runtime's buffers
@@ -762,6 +772,7 @@ class NeuralZipRuntime:
 
     def _decode_block(self, block_name, _module=None, _args=(), _kwargs=None):
         if self._segmenting is not None:   # a segmented capture: a new graph starts here, nothing is decoded
+            self._marker = None
             self._segmenting._split(block_name)
             return
         self._eager_decodes = True
@@ -770,6 +781,7 @@ class NeuralZipRuntime:
             rows = self._token_rows(_args, _kwargs)
             if rows is not None and rows <= self.matvec_tokens:
                 self._fused.add(block_name)
+                self._marker = None
                 pending, self._pending = self._pending, None
                 if pending is not None:   # nothing may still write a slot once decoding resumes
                     _native.decode_schedule(None, None, pending[1], None, None, stream, None)
@@ -780,20 +792,23 @@ class NeuralZipRuntime:
         # no longer writes a slot), then decode this block unless prefetched
         wait = pending[1] if pending is not None else None
         inline = None if pending is not None and pending[0] == block_name else self._schedule_args[block_name]
-        ahead = ready = done = following = None
+        ahead = ready = done = following = after = None
         if self.side_stream is not None and not self._side_off:
             following = self._following[block_name]
             if following == block_name or (not self._wrap and following == self.units[0]):
                 following = None
             else:
-                # recorded after everything queued so far (the last readers of
-                # `following`'s slot included): the side stream overwrites the
-                # slot only then; later records of an event do not change
-                # waits already queued on it
+                # `ready` is recorded after everything queued so far (the last
+                # readers of `following`'s slot included): the side stream
+                # overwrites the slot only then, or after the previous hook's
+                # record where that suffices; later records of an event do not
+                # change waits already queued on it
                 ready, done = self._events[following]
                 ahead = self._schedule_args[following]
-        _native.decode_schedule(inline, ahead, wait, ready, done, stream, self._side_handle)
+                after = self._earlier_marker(following, stream)
+        _native.decode_schedule(inline, ahead, wait, ready, done, stream, self._side_handle, after)
         self._pending = (following, done) if following is not None else None
+        self._marker = (block_name, ready, stream) if following is not None else None
         if torch.is_grad_enabled():
             # the decodes overwrite workspace slots behind autograd's back: a
             # new version makes a backward that saved an earlier block's weight
@@ -801,8 +816,27 @@ class NeuralZipRuntime:
             for workspace in self.workspaces.values():
                 torch.autograd.graph.increment_version(workspace)
 
+    def _earlier_marker(self, following, stream):
+        """The event the previous hook recorded on `stream`, if the side
+        stream may decode `following` once the work queued before it has run,
+        else None (the side stream then waits for everything queued so far).
+
+        Since that record only the previous hook's unit has run on `stream`,
+        and a unit's kernels read its own slot only; so the record suffices
+        when that unit's slot is not `following`'s, which takes three or more
+        workspace slots. In host-bound generation the record has completed
+        by the time of the next hook, and waiting for a completed event costs
+        the host well under a microsecond, against about 20 for one recorded
+        in the same call (MI355X, ROCm 7.2)."""
+        marker = self._marker
+        if marker is None or marker[2] != stream or marker[1] is None:
+            return None
+        unit, event, _ = marker
+        return event if self.block_slot[unit] != self.block_slot[following] else None
+
     def drain(self):
         """Order the compute stream after any pending side-stream decode."""
+        self._marker = None
         if self._pending is not None:
             _native.decode_schedule(None, None, self._pending[1], None, None, _current_stream_handle(self.device),
                                     None)

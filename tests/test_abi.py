@@ -116,13 +116,18 @@ def test_decode_args_layout_and_schedule_checks():
     assert [getattr(_native.DecodeArgs, n).offset for n in names] == offsets and ctypes.sizeof(_native.DecodeArgs) == 64
     lib = _native.lib()
     one = _native.decode_args([(1, 2, 3, 4, 5, 2, 1, 0, 6, 0)])
-    assert lib.nz_decode_schedule(None, 1, None, 0, None, None, None, None, None) == -1
-    assert lib.nz_decode_schedule(None, 0, one, 1, None, None, None, None, None) == -1
+    assert lib.nz_decode_schedule(None, 1, None, 0, None, None, None, None, None, None) == -1
+    assert lib.nz_decode_schedule(None, 0, one, 1, None, None, None, None, None, None) == -1
+    # an ahead launch needs `done` and something for the side stream to wait for (`ready` or `after`)
+    token = ctypes.c_void_p(1)
+    assert lib.nz_decode_schedule(None, 0, one, 1, None, None, None, token, None, None) == -1
+    assert lib.nz_decode_schedule(None, 0, one, 1, None, None, token, None, None, None) == -1
+    assert lib.nz_decode_schedule(None, 0, one, 1, None, token, None, None, None, None) == -1
     bad = _native.decode_args([(1, 2, 3, 4, 5, 2, 1, 0, 6, 0)])
     bad[0].reserved = 1
-    assert lib.nz_decode_schedule(bad, 1, None, 0, None, None, None, None, None) == -1
+    assert lib.nz_decode_schedule(bad, 1, None, 0, None, None, None, None, None, None) == -1
     assert b"reserved" in lib.nz_last_error()
-    assert lib.nz_decode_schedule(None, 0, None, 0, None, None, None, None, None) == 0
+    assert lib.nz_decode_schedule(None, 0, None, 0, None, None, None, None, None, None) == 0
 
 
 def test_numpy_records_match_the_device_structs():

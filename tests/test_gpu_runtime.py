@@ -85,7 +85,7 @@ def test_prefetch_uses_distinct_slots_and_side_stream():
     setup = NeuralZipSetup(chunk_size=65536).build(named)
     runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
     order = runtime.export.block_order
-    assert len(order) == 5 and len({runtime.block_slot[n] for n in order}) == 3   # odd count: 3 slots
+    assert len(order) == 5 and len({runtime.block_slot[n] for n in order}) == 3
     for a, b in zip(order, order[1:] + order[:1]):
         assert runtime.block_slot[a] != runtime.block_slot[b]
     for _ in range(4):
@@ -111,6 +111,32 @@ def _run(blocks, x):
     for block in blocks:
         x = block(x)
     return x
+
+
+@pytest.mark.parametrize("slots", [3, 4])
+def test_prefetch_after_earlier_records_while_the_device_lags(slots):
+    """With three or more workspace slots the side stream waits for the
+    previous hook's record. Blocks with long GEMMs (the host runs ahead, so
+    those records are still pending when waited for) stay bitwise equal
+    over repeated forwards, with forwards alternating between two streams."""
+    model, reference, named = _block_stack(7, width=2048, seed=17)
+    setup = NeuralZipSetup(chunk_size=1 << 20).build(named)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0",
+                                      workspace_slots=slots)
+    assert runtime.prefetch and len(set(runtime.block_slot.values())) >= 3
+    x = torch.randn(16384, 2048, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        expected = _run(reference.blocks, x)
+        outs = [_run(model.blocks, x) for _ in range(4)]
+        other = torch.cuda.Stream()
+        for k in range(4):
+            stream = other if k % 2 else torch.cuda.current_stream()
+            stream.wait_stream(torch.cuda.current_stream() if k % 2 else other)
+            with torch.cuda.stream(stream):
+                outs.append(_run(model.blocks, x))
+        torch.cuda.current_stream().wait_stream(other)
+    for k, y in enumerate(outs):
+        assert exact(y, expected), f"forward {k}"
 
 
 def test_prefetch_out_of_order_and_overwritten_workspace():
@@ -301,7 +327,7 @@ def test_segmented_graph_replays_match_eager(n_blocks):
     (even and odd block counts)."""
     model, reference, named = _block_stack(n_blocks, seed=13)
     setup = NeuralZipSetup(chunk_size=65536).build(named)
-    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0")
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, setup), device="cuda:0", workspace_slots=2)
     assert runtime.prefetch and len(set(runtime.block_slot.values())) == (2 if n_blocks % 2 == 0 else 3)
     g = torch.Generator().manual_seed(6)
     inputs = [torch.randn(4, 512, generator=g).to(torch.bfloat16).cuda() for _ in range(4)]
