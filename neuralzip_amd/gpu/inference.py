@@ -46,6 +46,9 @@ GRAPH_PREFETCH_MIN_BYTES = 64 << 20
 # same call: about 20 us less host time per hook, and eager 8B batch-1 steps
 # 0.6 ms faster (MI355X, ROCm 7.2).
 DEFAULT_WORKSPACE_SLOTS = 3
+# Hook records kept for choosing the side stream's wait (enough for that many
+# slots plus two).
+MARKER_HISTORY = 8
 _GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
 # Tensor offsets in a workspace: 128 elements keeps views 256-byte aligned
 # and fragment starts 16-element aligned (the layout's vector alignment).
@@ -555,7 +558,7 @@ class NeuralZipRuntime:
                             if self.prefetch else {})
         weakref.finalize(self, _destroy_events, self.device, [e for pair in self._events.values() for e in pair])
         self._pending = None   # (unit name, event) decoded ahead on the side stream
-        self._marker = None    # (unit, event, stream): the last hook's record on the compute stream
+        self._markers = []     # (unit, event, stream) recorded by consecutive hooks, oldest first
         self._wrap = True      # the last unit's hook prefetches the first unit (the next forward's)
         self._side_off = False  # graph_capture() decodes on the compute stream only
         self._captured = False  # graph_capture() was used: graphs may hold this runtime's buffers
@@ -772,7 +775,7 @@ class NeuralZipRuntime:
 
     def _decode_block(self, block_name, _module=None, _args=(), _kwargs=None):
         if self._segmenting is not None:   # a segmented capture: a new graph starts here, nothing is decoded
-            self._marker = None
+            self._markers = []
             self._segmenting._split(block_name)
             return
         self._eager_decodes = True
@@ -781,7 +784,7 @@ class NeuralZipRuntime:
             rows = self._token_rows(_args, _kwargs)
             if rows is not None and rows <= self.matvec_tokens:
                 self._fused.add(block_name)
-                self._marker = None
+                self._markers = []
                 pending, self._pending = self._pending, None
                 if pending is not None:   # nothing may still write a slot once decoding resumes
                     _native.decode_schedule(None, None, pending[1], None, None, stream, None)
@@ -800,7 +803,7 @@ class NeuralZipRuntime:
             else:
                 # `ready` is recorded after everything queued so far (the last
                 # readers of `following`'s slot included): the side stream
-                # overwrites the slot only then, or after the previous hook's
+                # overwrites the slot only then, or after an earlier hook's
                 # record where that suffices; later records of an event do not
                 # change waits already queued on it
                 ready, done = self._events[following]
@@ -808,7 +811,17 @@ class NeuralZipRuntime:
                 after = self._earlier_marker(following, stream)
         _native.decode_schedule(inline, ahead, wait, ready, done, stream, self._side_handle, after)
         self._pending = (following, done) if following is not None else None
-        self._marker = (block_name, ready, stream) if following is not None else None
+        if following is None:
+            self._markers = []
+        else:
+            # Records of consecutive hooks; one of an event recorded again
+            # (and every older one) leaves: a wait names an event's latest record.
+            kept = self._markers[1 - MARKER_HISTORY:]
+            for k in range(len(kept) - 1, -1, -1):
+                if kept[k][1] is ready:
+                    kept = kept[k + 1:]
+                    break
+            self._markers = kept + [(block_name, ready, stream)]
         if torch.is_grad_enabled():
             # the decodes overwrite workspace slots behind autograd's back: a
             # new version makes a backward that saved an earlier block's weight
@@ -817,26 +830,31 @@ class NeuralZipRuntime:
                 torch.autograd.graph.increment_version(workspace)
 
     def _earlier_marker(self, following, stream):
-        """The event the previous hook recorded on `stream`, if the side
-        stream may decode `following` once the work queued before it has run,
-        else None (the side stream then waits for everything queued so far).
+        """The oldest event that recent hooks recorded on `stream` after
+        which the side stream may decode `following`, or None (the side
+        stream then waits for everything queued so far).
 
-        Since that record only the previous hook's unit has run on `stream`,
-        and a unit's kernels read its own slot only; so the record suffices
-        when that unit's slot is not `following`'s, which takes three or more
-        workspace slots. In host-bound generation the record has completed
-        by the time of the next hook, and waiting for a completed event costs
-        the host well under a microsecond, against about 20 for one recorded
-        in the same call (MI355X, ROCm 7.2)."""
-        marker = self._marker
-        if marker is None or marker[2] != stream or marker[1] is None:
-            return None
-        unit, event, _ = marker
-        return event if self.block_slot[unit] != self.block_slot[following] else None
+        After the record of hook k only the units of hooks k, k+1, ... up to
+        the previous one have run on `stream`, and a unit's kernels (and an
+        inline decode at its hook) touch its own slot only; so the record
+        suffices when none of those units holds `following`'s slot. With
+        three slots that is the previous hook's record, with four the one
+        before it, and so on. In host-bound generation such a record has
+        completed by the time of the next hook, and waiting for a completed
+        event costs the host well under a microsecond, against about 20 for
+        one recorded in the same call (MI355X, ROCm 7.2); in a captured
+        graph an older record lets the side stream start sooner."""
+        target = self.block_slot[following]
+        chosen = None
+        for unit, event, on in reversed(self._markers):
+            if on != stream or self.block_slot[unit] == target:
+                break
+            chosen = event
+        return chosen
 
     def drain(self):
         """Order the compute stream after any pending side-stream decode."""
-        self._marker = None
+        self._markers = []
         if self._pending is not None:
             _native.decode_schedule(None, None, self._pending[1], None, None, _current_stream_handle(self.device),
                                     None)

@@ -113,10 +113,10 @@ def _run(blocks, x):
     return x
 
 
-@pytest.mark.parametrize("slots", [3, 4])
+@pytest.mark.parametrize("slots", [3, 4, 5])
 def test_prefetch_after_earlier_records_while_the_device_lags(slots):
-    """With three or more workspace slots the side stream waits for the
-    previous hook's record. Blocks with long GEMMs (the host runs ahead, so
+    """With three or more workspace slots the side stream waits for an
+    earlier hook's record. Blocks with long GEMMs (the host runs ahead, so
     those records are still pending when waited for) stay bitwise equal
     over repeated forwards, with forwards alternating between two streams."""
     model, reference, named = _block_stack(7, width=2048, seed=17)

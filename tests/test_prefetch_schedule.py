@@ -87,7 +87,7 @@ def fake_runtime(n_units, cycle, monkeypatch):
     rt.block_slot = _unit_slots(order, cycle)
     rt._following = {name: order[(i + 1) % len(order)] for i, name in enumerate(order)}
     rt._segmenting, rt._eager_decodes, rt._matvec_blocks, rt._fused = None, False, frozenset(), set()
-    rt._pending, rt._marker, rt._wrap, rt._side_off = None, None, True, False
+    rt._pending, rt._markers, rt._wrap, rt._side_off = None, [], True, False
     rt._schedule_args = {u: ("args", u) for u in order}
     rt._events = {u: (("ready", u), ("done", u)) for u in order}
     rt.side_stream, rt._side_handle, rt.device, rt.workspaces = object(), "side", None, {}
@@ -136,6 +136,30 @@ def test_three_slots_use_the_previous_record_for_every_hook_after_the_first(monk
     assert model.after_used == 3 * 33 - 1
 
 
+@pytest.mark.parametrize("cycle", [3, 4, 5, 6])
+def test_more_slots_wait_for_older_records(cycle, monkeypatch):
+    """With `cycle` slots, a hook in the middle of a forward has the side
+    stream wait for the record made cycle - 2 hooks earlier: the oldest after
+    which no queued block holds the slot being refilled."""
+    rt, model, current = fake_runtime(33, cycle, monkeypatch)
+    calls = []
+    schedule = model.schedule
+
+    def spy(inline, ahead, wait, ready, done, stream, side, after=None):
+        calls.append(after)
+        schedule(inline, ahead, wait, ready, done, stream, side, after)
+    monkeypatch.setattr(_native, "decode_schedule", spy)
+    order = rt.units
+    with torch.no_grad():
+        for _ in range(2):
+            for unit in order:
+                rt._decode_block(unit)
+                model.block_runs(unit)
+    for i in range(cycle, len(order) - cycle):
+        # hook w records ("ready", unit w + 1)
+        assert calls[len(order) + i] == ("ready", order[i - (cycle - 2) + 1]), i
+
+
 def test_two_slots_wait_for_a_record_made_in_the_same_call(monkeypatch):
     """Units 0..31 alternate two slots and the last takes a third: only the
     hooks next to the last unit may use the earlier record."""
@@ -148,11 +172,12 @@ def test_two_slots_wait_for_a_record_made_in_the_same_call(monkeypatch):
     assert model.after_used == 2 * 3 - 1
 
 
-def test_a_planted_rule_that_ignores_the_slots_is_caught(monkeypatch):
-    rt, model, current = fake_runtime(8, 2, monkeypatch)
-
-    def careless(self, following, stream):
-        return self._marker[1] if self._marker is not None else None
+@pytest.mark.parametrize("cycle, careless", [
+    (2, lambda self, following, stream: self._markers[-1][1] if self._markers else None),   # previous record
+    (4, lambda self, following, stream: self._markers[0][1] if self._markers else None),    # oldest record
+])
+def test_a_planted_rule_that_ignores_the_slots_is_caught(cycle, careless, monkeypatch):
+    rt, model, current = fake_runtime(9, cycle, monkeypatch)
     monkeypatch.setattr(NeuralZipRuntime, "_earlier_marker", careless)
     with torch.no_grad(), pytest.raises(AssertionError, match="overlaps"):
         for unit in rt.units * 2:
