@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define NZ_ABI_VERSION 10
+#define NZ_ABI_VERSION 11
 
 enum nz_status {
     NZ_OK = 0,

@@ -81,7 +81,7 @@ class _Totals(ctypes.Structure):
 
 _lib = None
 # The C ABI version (NZ_ABI_VERSION of include/neuralzip_hip.h) these bindings follow.
-ABI_VERSION = 10
+ABI_VERSION = 11
 # Activation rows one fused matrix-vector product takes (NZ_MATVEC_MAX_BATCH).
 MATVEC_MAX_BATCH = 4
 # Weights one fused product takes (NZ_MATVEC_MAX_WEIGHTS).
