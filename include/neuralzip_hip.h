@@ -174,14 +174,19 @@ int nz_decode_launch(const void* base, const nz_frag_desc* frags, const nz_tile*
 
 /* Flags of nz_decode_launch_ex. */
 #define NZ_DECODE_CACHED_STORES 1u   /* ordinary output stores (default: streaming) */
+#define NZ_DECODE_HALF_GROUPS 2u     /* workgroups of 8 wavefronts (default: 16) */
 
 /* nz_decode_launch with flags. NZ_DECODE_CACHED_STORES writes the decoded
  * words with ordinary stores, which leave them in the L2 and the Infinity
  * Cache for a consumer that runs right after the decode (a weight decoded
  * just before its own GEMM); the default streaming stores suit decodes
- * whose output is read later. Same reference counterpart as
- * nz_decode_launch (decoder.py:193-208), whose kernel always stores through
- * the caches. */
+ * whose output is read later. NZ_DECODE_HALF_GROUPS launches workgroups of
+ * 8 wavefronts (about 56 KB of LDS each) instead of 16 (77 KB), for a decode
+ * that runs beside another stream's kernels: one per CU leaves each CU most
+ * of its wavefront slots and LDS (the segments then come from a plan for as
+ * many workgroups). It takes streaming stores only. Same reference
+ * counterpart as nz_decode_launch (decoder.py:193-208), whose kernel always
+ * stores through the caches. */
 int nz_decode_launch_ex(const void* base, const nz_frag_desc* frags, const nz_tile* tiles, const nz_work* segments,
                         uint32_t n_segments, int element_size, int bit_reorder, int long_codes, void* out,
                         uint32_t flags, void* stream);

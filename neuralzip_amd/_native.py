@@ -271,8 +271,10 @@ def decode_slots(element_size, bit_reorder, long_codes):
     return n.value
 
 
-# nz_decode_launch_ex flag: ordinary output stores (the words stay in the caches)
+# nz_decode_launch_ex flags: ordinary output stores (the words stay in the
+# caches); workgroups of 8 wavefronts instead of 16
 DECODE_CACHED_STORES = 1
+DECODE_HALF_GROUPS = 2
 
 
 def decode_launch(base_ptr, frags_ptr, tiles_ptr, segments_ptr, n_segments, element_size, bit_reorder, long_codes,

@@ -37,7 +37,7 @@ using nz_capi::set_error;
 
 extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes, void* out,
-                                    int cached, void* stream, char* message, size_t message_size);
+                                    int cached, int half, void* stream, char* message, size_t message_size);
 extern "C" int nz_hip_decode_slots(int element_size, int bit_reorder, int long_codes, int* out, char* message,
                                    size_t message_size);
 extern "C" int nz_hip_event_create(void** event, char* message, size_t message_size);
@@ -231,10 +231,14 @@ int nz_decode_launch_ex(const void* base, const nz_frag_desc* frags, const nz_ti
                         uint32_t flags, void* stream) {
     if (n_segments && (!base || !frags || !tiles || !segments || !out))
         return set_error(nz::kInvalidArgument, "Null decode argument.");
-    if (flags & ~uint32_t(NZ_DECODE_CACHED_STORES)) return set_error(nz::kInvalidArgument, "Unknown decode flags.");
+    if (flags & ~uint32_t(NZ_DECODE_CACHED_STORES | NZ_DECODE_HALF_GROUPS))
+        return set_error(nz::kInvalidArgument, "Unknown decode flags.");
+    if ((flags & NZ_DECODE_CACHED_STORES) && (flags & NZ_DECODE_HALF_GROUPS))
+        return set_error(nz::kInvalidArgument, "Half-size decode groups take streaming stores only.");
     char message[256] = {0};
     const int rc = nz_hip_decode_launch(base, frags, tiles, segments, n_segments, element_size, bit_reorder,
-                                        long_codes, out, (flags & NZ_DECODE_CACHED_STORES) != 0, stream, message,
+                                        long_codes, out, (flags & NZ_DECODE_CACHED_STORES) != 0,
+                                        (flags & NZ_DECODE_HALF_GROUPS) != 0, stream, message,
                                         sizeof message);
     if (rc) return set_error(rc, message);
     return 0;

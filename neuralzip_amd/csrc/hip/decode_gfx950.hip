@@ -33,15 +33,14 @@ namespace {
 
 // Wavefronts per workgroup: 16 with the 36 KB LUT image and 2 KB of staging
 // per wavefront lets two workgroups (8 wavefronts per SIMD) share a CU's LDS.
-#ifndef NZ_GROUP_WAVES
-#define NZ_GROUP_WAVES 16
-#endif
-// Minimum wavefronts per SIMD the register allocator must allow.
-#ifndef NZ_WAVES_PER_EU
-#define NZ_WAVES_PER_EU 8
-#endif
-constexpr int kWaves = NZ_GROUP_WAVES;
-constexpr int kThreads = kWaves * NZ_WAVE;
+// A decode that runs beside other kernels uses workgroups of 8 (half-size
+// groups): one per CU leaves the CU three quarters of its wavefront slots
+// and most of its LDS.
+constexpr int kWaves = 16;
+constexpr int kHalfWaves = 8;
+// Minimum wavefronts per SIMD the register allocator must allow: the LDS of
+// two workgroups per CU allows 8 at 16 wavefronts per group and 4 at 8.
+constexpr int waves_per_eu(int waves) { return waves == kWaves ? 8 : 4; }
 
 // One element from its exponent byte and its raw lane bytes `raw`
 // (lane k in byte k).
@@ -192,14 +191,14 @@ __device__ __forceinline__ void raw_segment(const uint8_t* base, const nz_frag_d
 // Launch: one workgroup per segment (segments are cut to equal work, about
 // as many as the device runs at once); its wavefronts claim the segment's
 // tiles one at a time, so a wavefront with cheap tiles takes more of them.
-template <int ES, bool REORDER, bool LONG, bool CACHED>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NZ_WAVES_PER_EU)))
+template <int ES, bool REORDER, bool LONG, bool CACHED, int WAVES>
+__global__ __launch_bounds__(WAVES * NZ_WAVE) __attribute__((amdgpu_waves_per_eu(waves_per_eu(WAVES))))
 void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __restrict__ frags,
                       const nz_tile* __restrict__ tiles, const nz_work* __restrict__ segs,
                       uint8_t* __restrict__ out) {
     using G = Geometry<ES>;
     __shared__ __align__(16) uint32_t s_lut[NZ_LUT_MAX_WORDS];
-    __shared__ __align__(16) uint8_t s_stage[kWaves][G::kStage];
+    __shared__ __align__(16) uint8_t s_stage[WAVES][G::kStage];
     __shared__ uint32_t s_claim;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / NZ_WAVE);
     const uint32_t lane = threadIdx.x % NZ_WAVE;
@@ -215,7 +214,7 @@ void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
     // malformed one from overwriting the staging areas behind s_lut
     const uint32_t words = min(reinterpret_cast<const uint32_t*>(img)[2], uint32_t(NZ_LUT_MAX_WORDS));
     uint4* dst = reinterpret_cast<uint4*>(s_lut);
-    for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += kThreads) dst[i] = img[i];
+    for (uint32_t i = threadIdx.x; i < (words + 3) / 4; i += WAVES * NZ_WAVE) dst[i] = img[i];
     __syncthreads();
     // Codebooks whose codes all fit the primary table run the loop without
     // the escape check (long-code codebooks always have escapes).
@@ -234,16 +233,18 @@ void nz_decode_kernel(const uint8_t* __restrict__ base, const nz_frag_desc* __re
 
 template <int ES, bool REORDER, bool LONG>
 hipError_t launch(const void* base, const void* frags, const void* tiles, const void* segs, uint32_t n_segs,
-                  void* out, bool cached, hipStream_t stream) {
-    auto args = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, dim3(n_segs), dim3(kThreads), 0, stream, static_cast<const uint8_t*>(base),
+                  void* out, bool cached, bool half, hipStream_t stream) {
+    auto args = [&](auto kernel, int waves) {
+        hipLaunchKernelGGL(kernel, dim3(n_segs), dim3(waves * NZ_WAVE), 0, stream, static_cast<const uint8_t*>(base),
                            static_cast<const nz_frag_desc*>(frags), static_cast<const nz_tile*>(tiles),
                            static_cast<const nz_work*>(segs), static_cast<uint8_t*>(out));
     };
-    if (cached)
-        args(nz_decode_kernel<ES, REORDER, LONG, true>);
+    if (half)   // streaming stores only: half-size groups serve decodes read later
+        args(nz_decode_kernel<ES, REORDER, LONG, false, kHalfWaves>, kHalfWaves);
+    else if (cached)
+        args(nz_decode_kernel<ES, REORDER, LONG, true, kWaves>, kWaves);
     else
-        args(nz_decode_kernel<ES, REORDER, LONG, false>);
+        args(nz_decode_kernel<ES, REORDER, LONG, false, kWaves>, kWaves);
     return hipGetLastError();
 }
 
@@ -253,8 +254,8 @@ hipError_t slots(int* out) {
     hipError_t rc = hipGetDevice(&device);
     if (rc == hipSuccess) rc = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
     if (rc == hipSuccess)
-        rc = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nz_decode_kernel<ES, REORDER, LONG, false>, kThreads,
-                                                          0);
+        rc = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nz_decode_kernel<ES, REORDER, LONG, false, kWaves>,
+                                                          kWaves * NZ_WAVE, 0);
     *out = cus * per_cu;
     return rc;
 }
@@ -265,11 +266,15 @@ hipError_t slots(int* out) {
 // (stream-ordered, asynchronous). Returns 0 or a negative error code.
 extern "C" int nz_hip_decode_launch(const void* base, const void* frags, const void* tiles, const void* segs,
                                     uint32_t n_segs, int element_size, int bit_reorder, int long_codes, void* out,
-                                    int cached, void* stream, char* message, size_t message_size) {
+                                    int cached, int half, void* stream, char* message, size_t message_size) {
+    if (cached && half) {
+        snprintf(message, message_size, "Half-size decode groups take streaming stores only.");
+        return -1;
+    }
     if (n_segs == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t rc;
-#define NZ_LAUNCH(E, R, L) launch<E, R, L>(base, frags, tiles, segs, n_segs, out, cached != 0, st)
+#define NZ_LAUNCH(E, R, L) launch<E, R, L>(base, frags, tiles, segs, n_segs, out, cached != 0, half != 0, st)
     if (element_size == 2 && bit_reorder)
         rc = long_codes ? NZ_LAUNCH(2, true, true) : NZ_LAUNCH(2, true, false);
     else if (element_size == 2)

@@ -126,11 +126,16 @@ class HIPDecoder:
         _native.lib()
         return group.layout
 
-    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), slots=SLOTS, cached_stores=False):
+    def prepare_batch(self, store, fragment_indices, dtype, output, outputs=(), slots=SLOTS, cached_stores=False,
+                      half_groups=False):
         """Tiles of `fragment_indices` (one dtype and kind), ordered so that
         fragments of one LUT are adjacent, and their launch plan. With
         `cached_stores` the launch writes with ordinary stores, for a
-        consumer that reads the words right after the decode."""
+        consumer that reads the words right after the decode; with
+        `half_groups` it runs workgroups of 8 wavefronts instead of 16, for a
+        decode beside another stream's kernels (streaming stores only)."""
+        if cached_stores and half_groups:
+            raise ValueError("Half-size decode groups take streaming stores only.")
         fragment_indices = list(fragment_indices)
         if not fragment_indices:
             raise ValueError("A decode batch must contain at least one group.")
@@ -150,7 +155,8 @@ class HIPDecoder:
         segments_t = torch.from_numpy(segments.view(np.uint8).copy()).to(device)
         args = (store.buffer.data_ptr(), store.frags.data_ptr(), tiles_t.data_ptr(), segments_t.data_ptr(),
                 len(segments), key[0], int(key[1]), int(key[2]), output.data_ptr(),
-                _native.DECODE_CACHED_STORES if cached_stores else 0)
+                (_native.DECODE_CACHED_STORES if cached_stores else 0)
+                | (_native.DECODE_HALF_GROUPS if half_groups else 0))
         return PreparedBatch((tiles_t, segments_t), device, key, (len(segments),), len(segments), store, output,
                              tuple(outputs), algorithmic_bytes(store.descs[fragment_indices], dtype), args)
 

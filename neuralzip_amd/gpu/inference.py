@@ -46,6 +46,14 @@ GRAPH_PREFETCH_MIN_BYTES = 64 << 20
 # same call: about 20 us less host time per hook, and eager 8B batch-1 steps
 # 0.6 ms faster (MI355X, ROCm 7.2).
 DEFAULT_WORKSPACE_SLOTS = 3
+# Side-stream decodes of blocks below this many decoded bytes on average run
+# as half-size workgroups (8 wavefronts), one per CU: such blocks' compute is
+# mostly short kernels that leave HBM idle, and they keep more of each CU.
+# Larger blocks keep full workgroups on three CUs in four, whose decode
+# throughput a step bound by HBM traffic needs. Graph-replayed steps
+# (MI355X): Llama-3-8B, 436 MB blocks, 13.71 against 13.88 ms; Llama-3-70B,
+# 1.7 GB blocks, 76.0 against 77.2-79.1 ms.
+HALF_GROUP_MAX_BYTES = 1 << 30
 # Hook records kept for choosing the side stream's wait (enough for that many
 # slots plus two).
 MARKER_HISTORY = 8
@@ -518,32 +526,42 @@ class NeuralZipRuntime:
             self.store = _store[1]
         else:
             self.store = gpu_decoder.DeviceStore(exported.codebooks, tensors, self.device)
-        self._prepared_batches = defaultdict(list)
+        # Launch plans: `_prepared_batches` for decodes on the compute stream
+        # and `_ahead_batches` for prefetches on the side stream (the same
+        # plans unless the prefetches run as half-size workgroups).
+        self._prepared_batches, self._ahead_batches = defaultdict(list), defaultdict(list)
         self.algorithmic_bytes = {}
+        decoded = sum(g.encoded.raw_bytes for g in exported.groups)
+        half_groups = (self.prefetch and granularity == "block"
+                       and decoded < HALF_GROUP_MAX_BYTES * max(len(order), 1))
+        cus = self._compute_units()
         for (name, dtype), frags in by_unit.items():
             spec = DTYPES[dtype]
             kinds = defaultdict(list)
             for f in frags:
                 kinds[int(self.store.descs[f]["kind"]) == KIND_LONG].append(f)
             for long_codes, members in sorted(kinds.items()):
-                slots = decode_slots
-                if slots is None:
-                    # A decode that runs beside the compute stream's kernels
-                    # gets one workgroup on three CUs in four: its workgroups
-                    # hold half of a CU's LDS and wavefront slots, and kernels
-                    # of the compute stream that share a CU with one run
-                    # slower. A decode on the compute stream alone gets one
-                    # workgroup per CU, its fastest count there.
-                    resident = self._decoder.slots(self.device, (spec.element_size, bool(spec.bit_reorder),
-                                                                 bool(long_codes)))
-                    cus = self._compute_units()
-                    slots = max(1, min(resident, cus * 3 // 4 if self.prefetch else cus))
-                # a weight decoded right before its own GEMM is read back at
-                # once: ordinary stores leave it in the caches for that read
-                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype], slots=slots,
-                                                    cached_stores=granularity == "linear")
+                resident = self._decoder.slots(self.device, (spec.element_size, bool(spec.bit_reorder),
+                                                             bool(long_codes)))
+
+                def prepare(share, half):
+                    # a weight decoded right before its own GEMM is read back
+                    # at once: ordinary stores leave it in the caches for that read
+                    return self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype],
+                                                       slots=decode_slots or max(1, min(resident, share)),
+                                                       cached_stores=granularity == "linear", half_groups=half)
+                # A decode on the compute stream alone gets one full workgroup
+                # (16 wavefronts) per CU, its fastest count there. One beside
+                # the compute stream's kernels gets one half-size workgroup per
+                # CU (HALF_GROUP_MAX_BYTES) or one full workgroup on three CUs
+                # in four: the kernels that share a CU with a decode run slower.
+                batch = prepare(cus * 3 // 4 if self.prefetch and not half_groups else cus, False)
                 self._prepared_batches[name].append(batch)
+                if half_groups:
+                    self._ahead_batches[name].append(prepare(cus, True))
                 self.algorithmic_bytes[name] = self.algorithmic_bytes.get(name, 0) + batch.algorithmic_bytes
+        if not half_groups:
+            self._ahead_batches = self._prepared_batches
         self._groups_by_block = defaultdict(list)
         for group in exported.groups:
             self._groups_by_block[group.block_name].append(group)
@@ -553,6 +571,8 @@ class NeuralZipRuntime:
         # a single nz_decode_schedule call
         self._schedule_args = {name: _native.decode_args([b.launch_args for b in batches])
                                for name, batches in self._prepared_batches.items()}
+        self._ahead_args = self._schedule_args if self._ahead_batches is self._prepared_batches else {
+            name: _native.decode_args([b.launch_args for b in batches]) for name, batches in self._ahead_batches.items()}
         with torch.cuda.device(self.device):
             self._events = ({name: (_native.event_create(), _native.event_create()) for name in order}
                             if self.prefetch else {})
@@ -807,7 +827,7 @@ class NeuralZipRuntime:
                 # record where that suffices; later records of an event do not
                 # change waits already queued on it
                 ready, done = self._events[following]
-                ahead = self._schedule_args[following]
+                ahead = self._ahead_args[following]
                 after = self._earlier_marker(following, stream)
         _native.decode_schedule(inline, ahead, wait, ready, done, stream, self._side_handle, after)
         self._pending = (following, done) if following is not None else None
@@ -896,6 +916,7 @@ class NeuralZipRuntime:
                 and settings["workspace_slots"] == self.workspace_slots)
         store = (self._store_key, self.store) if same else None
         self.store, self._prepared_batches, self._schedule_args = None, defaultdict(list), {}
+        self._ahead_batches, self._ahead_args = defaultdict(list), {}
         self._matvec, self._group_plans, self._outputs, self._partials = {}, {}, {}, None
         runtime = type(self)(self.model, self.export, self.device, _store=store, **settings)
         runtime._grad_flags = getattr(self, "_grad_flags", {})
@@ -1050,7 +1071,7 @@ class SegmentedGraph:
         with torch.cuda.device(runtime.device):
             self._ready = [torch.cuda.Event() for _ in units]
             self._done = [torch.cuda.Event() for _ in units]
-        self._launches = [runtime._schedule_args[unit] if unit is not None else None for unit in units]
+        self._launches = [runtime._ahead_args[unit] if unit is not None else None for unit in units]
 
     def replay(self):
         runtime = self.runtime

@@ -128,6 +128,11 @@ def test_decode_args_layout_and_schedule_checks():
     assert lib.nz_decode_schedule(bad, 1, None, 0, None, None, None, None, None, None) == -1
     assert b"reserved" in lib.nz_last_error()
     assert lib.nz_decode_schedule(None, 0, None, 0, None, None, None, None, None, None) == 0
+    # nz_decode_launch_ex: unknown flags, and half-size groups with cached stores, fail before any HIP call
+    for flags, message in ((4, b"Unknown decode flags"), (_native.DECODE_CACHED_STORES | _native.DECODE_HALF_GROUPS,
+                                                         b"streaming stores only")):
+        assert lib.nz_decode_launch_ex(None, None, None, None, 0, 2, 1, 0, None, flags, None) == -1
+        assert message in lib.nz_last_error()
 
 
 def test_numpy_records_match_the_device_structs():

@@ -17,11 +17,12 @@ pytestmark = pytest.mark.gpu
 
 
 def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, slots=None, launches=2,
-            interleaved=False):
+            interleaved=False, flags=0):
     """Decodes every tile (one launch per kind) `launches` times in a row,
     poisoning the workspace before each round; returns the workspace bytes
     of every round and the plans. `interleaved` plans with
-    nz_plan_work_interleaved (and uploads the tiles in its order)."""
+    nz_plan_work_interleaved (and uploads the tiles in its order); `flags`
+    go to nz_decode_launch_ex."""
     device = torch.device("cuda:0")
     out = torch.full((workspace_elements * element_size + 64,), 0xA5, dtype=torch.uint8, device=device)
     base_t = torch.from_numpy(base).to(device)
@@ -47,20 +48,20 @@ def run_gpu(base, descs, tiles, element_size, bit_reorder, workspace_elements, s
         for long_codes, sel, segments, (tiles_t, segments_t) in plans:
             _native.decode_launch(base_t.data_ptr(), frags_t.data_ptr(), tiles_t.data_ptr(), segments_t.data_ptr(),
                                   len(segments), element_size, bit_reorder, long_codes, out.data_ptr(),
-                                  stream.cuda_stream)
+                                  stream.cuda_stream, flags)
         torch.cuda.synchronize(device)
         rounds.append(out.cpu().numpy())
     return rounds, plans
 
 
-def check_case(tensors, codebooks, dtype, repeats=1, slots=None, interleaved=False):
+def check_case(tensors, codebooks, dtype, repeats=1, slots=None, interleaved=False, flags=0):
     spec = DTYPES[dtype]
     enc = Encoded(tensors, codebooks)
     base, descs, tiles = enc.host_image()
     size = max(off + raw.size // spec.element_size for raw, _, _, _, off in tensors)
     for _ in range(repeats):
         rounds, plans = run_gpu(base, descs, tiles, spec.element_size, spec.bit_reorder, size, slots,
-                                interleaved=interleaved)
+                                interleaved=interleaved, flags=flags)
         emu = np.full_like(rounds[0], 0xA5)
         for _, sel, segments, _ in plans:
             _native.emulate_decode(base, descs, sel, segments, spec.element_size, spec.bit_reorder, emu)
@@ -122,6 +123,28 @@ def test_interleaved_plan_is_bit_exact(slots):
     long_raw = segment_tensor(torch.float32, symbols)
     check_case([(long_raw, torch.float32, 1 << 20, [0], 0)], {0: book}, torch.float32, repeats=2, slots=slots,
                interleaved=True)
+
+
+@pytest.mark.parametrize("slots", [256, 3, 100000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_half_size_groups_are_bit_exact(dtype, slots):
+    """NZ_DECODE_HALF_GROUPS (workgroups of 8 wavefronts, the runtime's
+    side-stream decodes): two codebooks and a raw chunk at an odd workspace
+    offset, and 56-bit codes, under the interleaved plan, against the
+    original words and the CPU emulation."""
+    g = torch.Generator().manual_seed(12)
+    raw = (torch.randn(301, 1500, generator=g) * 0.03).to(dtype).view(torch.uint8).numpy().reshape(-1)
+    books = {0: _native.Codebook(singleton_header(raw, dtype)),
+             1: _native.Codebook(singleton_header(raw[:40000], dtype, prior=3))}
+    per = DTYPES[dtype].element_size
+    ids = [(0, 1, -1)[j % 3] for j in range(-(-raw.size // per // 65536))]
+    check_case([(raw, dtype, 65536, ids, 37)], books, dtype, slots=slots, interleaved=True,
+               flags=_native.DECODE_HALF_GROUPS)
+    vocab = bytes((127, 127, 125, 126))
+    book = _native.Codebook(b"NZM1" + segment_lengths(56), vocab)
+    symbols = np.array([127] * 70000 + list(range(256)) * 3 + [125, 126, 126], dtype=np.uint8)
+    check_case([(segment_tensor(dtype, symbols), dtype, 1 << 20, [0], 0)], {0: book}, dtype, repeats=2,
+               slots=slots, interleaved=True, flags=_native.DECODE_HALF_GROUPS)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])

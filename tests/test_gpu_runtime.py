@@ -193,8 +193,10 @@ def test_graph_replays_match_eager(prefetch):
 
 @pytest.mark.parametrize("decode_slots", [None, 512, 3])
 def test_block_launch_workgroups(decode_slots):
-    """Block launches that prefetch use one workgroup on three CUs in four
-    by default, or the count asked for; every count decodes the same bits."""
+    """Prefetches of small blocks use half-size workgroups (8 wavefronts),
+    one per CU by default, or the count asked for; decodes on the compute
+    stream use full workgroups, one per CU by default. Every count decodes
+    the same bits."""
     from neuralzip_amd import _native
     model = nn.Module()
     model.blocks = nn.ModuleList([nn.Sequential(nn.Linear(4096, 4096, bias=False, dtype=torch.bfloat16),
@@ -213,17 +215,41 @@ def test_block_launch_workgroups(decode_slots):
                                       decode_slots=decode_slots)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     resident = _native.decode_slots(2, 1, 0)
-    for batches in runtime._prepared_batches.values():
-        for batch in batches:
+    assert runtime.prefetch and runtime._ahead_batches is not runtime._prepared_batches
+    for plans, half in ((runtime._ahead_batches, True), (runtime._prepared_batches, False)):
+        for batch in (b for batches in plans.values() for b in batches):
+            assert bool(batch.launch_args[-1] & _native.DECODE_HALF_GROUPS) == half
             if decode_slots is None:
-                assert runtime.prefetch
-                assert 1 < batch.n_segments <= min(cus * 3 // 4, resident)
+                assert 1 < batch.n_segments <= min(cus, resident)
             elif decode_slots == 3:   # a launch has at least one segment per codebook run
                 assert batch.n_segments <= max(3, len(runtime.export.codebooks) + 1)
             else:
                 assert min(cus, resident) < batch.n_segments <= decode_slots
     for _ in range(3):
         assert exact(model.blocks[1](model.blocks[0](x)), expected)
+
+
+def test_large_blocks_prefetch_with_full_workgroups(monkeypatch):
+    """Blocks of HALF_GROUP_MAX_BYTES or more on average (here the limit is
+    lowered to one byte) prefetch with full workgroups on three CUs in four,
+    and decode the same bits."""
+    from neuralzip_amd import _native
+    from neuralzip_amd.gpu import inference
+    monkeypatch.setattr(inference, "HALF_GROUP_MAX_BYTES", 1)
+    model, reference, named = _block_stack(3, width=2048, seed=21)
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, NeuralZipSetup().build(named)),
+                                      device="cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    resident = _native.decode_slots(2, 1, 0)
+    assert runtime._ahead_batches is runtime._prepared_batches
+    for batches in runtime._prepared_batches.values():
+        for batch in batches:
+            assert not batch.launch_args[-1] & _native.DECODE_HALF_GROUPS
+            assert 1 < batch.n_segments <= min(cus * 3 // 4, resident)
+    x = torch.randn(64, 2048, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).cuda()
+    expected = _run(reference.blocks, x)
+    for _ in range(3):
+        assert exact(_run(model.blocks, x), expected)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])

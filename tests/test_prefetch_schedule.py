@@ -89,6 +89,7 @@ def fake_runtime(n_units, cycle, monkeypatch):
     rt._segmenting, rt._eager_decodes, rt._matvec_blocks, rt._fused = None, False, frozenset(), set()
     rt._pending, rt._markers, rt._wrap, rt._side_off = None, [], True, False
     rt._schedule_args = {u: ("args", u) for u in order}
+    rt._ahead_args = rt._schedule_args
     rt._events = {u: (("ready", u), ("done", u)) for u in order}
     rt.side_stream, rt._side_handle, rt.device, rt.workspaces = object(), "side", None, {}
     model = StreamModel(rt)
