@@ -470,7 +470,10 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                    "peak_allocated_uncompressed_gib": round(base_peak / 2**30, 2),
                    "peak_allocated_neuralzip_gib": round(nz_peak / 2**30, 2),
                    "fragments": len(exported.groups),
-                   "prefetch": runtime.prefetch, "decode_slots": slots or "3/4 of the CUs (prefetch) or one per CU",
+                   "prefetch": runtime.prefetch,
+                   "decode_slots": slots or ("side stream: one half-size workgroup per CU (blocks under 1 GiB) or one "
+                                             "full workgroup on 3/4 of the CUs; compute stream: one full per CU"),
+                   "side_stream_half_groups": runtime._ahead_batches is not runtime._prepared_batches,
                    "workspace_slots": len(set(runtime.block_slot.values())), **matvec_info},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),
