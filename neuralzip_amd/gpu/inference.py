@@ -54,8 +54,9 @@ DEFAULT_WORKSPACE_SLOTS = 3
 # (MI355X): Llama-3-8B, 436 MB blocks, 13.71 against 13.88 ms; Llama-3-70B,
 # 1.7 GB blocks, 76.0 against 77.2-79.1 ms.
 HALF_GROUP_MAX_BYTES = 1 << 30
-# Hook records kept for choosing the side stream's wait (enough for that many
-# slots plus two).
+# Hook records kept for choosing the side stream's wait: with c workspace
+# slots the oldest record that can serve is c - 2 hooks back, so 8 records
+# serve up to 10 slots.
 MARKER_HISTORY = 8
 _GPU_WEIGHT_TYPES = (nn.Linear, nn.Conv2d, Conv1D)
 # Tensor offsets in a workspace: 128 elements keeps views 256-byte aligned
@@ -543,22 +544,22 @@ class NeuralZipRuntime:
             for long_codes, members in sorted(kinds.items()):
                 resident = self._decoder.slots(self.device, (spec.element_size, bool(spec.bit_reorder),
                                                              bool(long_codes)))
-
-                def prepare(share, half):
-                    # a weight decoded right before its own GEMM is read back
-                    # at once: ordinary stores leave it in the caches for that read
-                    return self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype],
-                                                       slots=decode_slots or max(1, min(resident, share)),
-                                                       cached_stores=granularity == "linear", half_groups=half)
                 # A decode on the compute stream alone gets one full workgroup
                 # (16 wavefronts) per CU, its fastest count there. One beside
                 # the compute stream's kernels gets one half-size workgroup per
                 # CU (HALF_GROUP_MAX_BYTES) or one full workgroup on three CUs
                 # in four: the kernels that share a CU with a decode run slower.
-                batch = prepare(cus * 3 // 4 if self.prefetch and not half_groups else cus, False)
+                # A weight decoded right before its own GEMM is read back at
+                # once: ordinary stores leave it in the caches for that read.
+                share = cus * 3 // 4 if self.prefetch and not half_groups else cus
+                batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype],
+                                                    slots=decode_slots or max(1, min(resident, share)),
+                                                    cached_stores=granularity == "linear")
                 self._prepared_batches[name].append(batch)
                 if half_groups:
-                    self._ahead_batches[name].append(prepare(cus, True))
+                    self._ahead_batches[name].append(self._decoder.prepare_batch(
+                        self.store, members, spec, self.workspaces[dtype],
+                        slots=decode_slots or max(1, min(resident, cus)), half_groups=True))
                 self.algorithmic_bytes[name] = self.algorithmic_bytes.get(name, 0) + batch.algorithmic_bytes
         if not half_groups:
             self._ahead_batches = self._prepared_batches
