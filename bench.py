@@ -472,7 +472,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                    "fragments": len(exported.groups),
                    "prefetch": runtime.prefetch,
                    "decode_slots": slots or ("side stream: one half-size workgroup per CU (blocks under 1 GiB) or one "
-                                             "full workgroup on 3/4 of the CUs; compute stream: one full per CU"),
+                                             "full workgroup on 7/8 of the CUs; compute stream: one full per CU"),
                    "side_stream_half_groups": runtime._ahead_batches is not runtime._prepared_batches,
                    "workspace_slots": len(set(runtime.block_slot.values())), **matvec_info},
         "uncompressed_tok_s": round(base_tok_s, 2),

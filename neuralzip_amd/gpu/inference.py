@@ -49,10 +49,11 @@ DEFAULT_WORKSPACE_SLOTS = 3
 # Side-stream decodes of blocks below this many decoded bytes on average run
 # as half-size workgroups (8 wavefronts), one per CU: such blocks' compute is
 # mostly short kernels that leave HBM idle, and they keep more of each CU.
-# Larger blocks keep full workgroups on three CUs in four, whose decode
+# Larger blocks keep full workgroups on seven CUs in eight, whose decode
 # throughput a step bound by HBM traffic needs. Graph-replayed steps
-# (MI355X): Llama-3-8B, 436 MB blocks, 13.71 against 13.88 ms; Llama-3-70B,
-# 1.7 GB blocks, 76.0 against 77.2-79.1 ms.
+# (MI355X): Llama-3-8B, 436 MB blocks, 13.60-13.71 against 13.88 ms (full
+# workgroups on 192 CUs); Llama-3-70B, 1.7 GB blocks, 75.5 ms (76.0 on 192
+# CUs) against 77.2-79.1 ms with half-size workgroups.
 HALF_GROUP_MAX_BYTES = 1 << 30
 # Hook records kept for choosing the side stream's wait: with c workspace
 # slots the oldest record that can serve is c - 2 hooks back, so 8 records
@@ -547,11 +548,11 @@ class NeuralZipRuntime:
                 # A decode on the compute stream alone gets one full workgroup
                 # (16 wavefronts) per CU, its fastest count there. One beside
                 # the compute stream's kernels gets one half-size workgroup per
-                # CU (HALF_GROUP_MAX_BYTES) or one full workgroup on three CUs
-                # in four: the kernels that share a CU with a decode run slower.
+                # CU (HALF_GROUP_MAX_BYTES) or one full workgroup on seven CUs
+                # in eight: the kernels that share a CU with a decode run slower.
                 # A weight decoded right before its own GEMM is read back at
                 # once: ordinary stores leave it in the caches for that read.
-                share = cus * 3 // 4 if self.prefetch and not half_groups else cus
+                share = cus * 7 // 8 if self.prefetch and not half_groups else cus
                 batch = self._decoder.prepare_batch(self.store, members, spec, self.workspaces[dtype],
                                                     slots=decode_slots or max(1, min(resident, share)),
                                                     cached_stores=granularity == "linear")
