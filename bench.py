@@ -20,6 +20,7 @@ model part runs first (about a minute).
 """
 import argparse
 import contextlib
+import gc
 import json
 import os
 import statistics
@@ -377,6 +378,10 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
     pass_ms = a.elapsed_time(b) / passes
     decoded_bytes = sum(g.encoded.raw_bytes for g in exported.groups)
     log(f"full decode pass: {pass_ms:.3f} ms, {decoded_bytes / pass_ms / 1e6:.0f} GB/s decoded")
+    # objects of the bf16 graph run (the captured graph's memory pool among
+    # them) may sit in reference cycles: collect them so that both peaks are
+    # measured from live tensors only
+    gc.collect()
     torch.cuda.empty_cache()
     torch.cuda.reset_peak_memory_stats(device)
     nz_s, nz_out = time_generate(model, ids, new_tokens)
