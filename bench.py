@@ -522,7 +522,7 @@ def model_summary(line):
             "peak_allocated_neuralzip_gib": line["config"]["peak_allocated_neuralzip_gib"]}
 
 
-def trace_summary(path, kernel="nz_decode_kernel<2, true, false, false>", steps=20):
+def trace_summary(path, kernel="nz_decode_kernel<2, true, false, false, 16>", steps=20):
     """Summary of a rocprofv3 kernel trace (CSV) of the default bench run: the
     durations of the last `steps` dispatches whose kernel name contains
     `kernel` (the timed steps, which end the run) and their mean, beside all
@@ -609,7 +609,7 @@ def main():
     parser.add_argument("--new-tokens", type=int, default=None, help="generated tokens (default: the model's)")
     parser.add_argument("--no-graph", action="store_true", help="model benchmark: eager generation only")
     parser.add_argument("--workspace-slots", type=int, default=None,
-                        help="model benchmark: workspace slots the decoded blocks take in turn (default 2)")
+                        help="model benchmark: workspace slots the decoded blocks take in turn (default 3)")
     parser.add_argument("--no-model", action="store_true",
                         help="default run: leave out the Llama-3-8B-shape bs=1 tok/s part of the line")
     parser.add_argument("--trace-summary", default=None, metavar="KERNEL_TRACE_CSV",
