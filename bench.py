@@ -478,7 +478,7 @@ def run_model(kind, batch=1, dtype_name="bf16", matvec=0, slots=None, prompt=Non
                    "prefetch": runtime.prefetch,
                    "decode_slots": slots or ("side stream: one half-size workgroup per CU (blocks under 1 GiB) or one "
                                              "full workgroup on 7/8 of the CUs; compute stream: one full per CU"),
-                   "side_stream_half_groups": runtime._ahead_batches is not runtime._prepared_batches,
+                   "side_stream_half_groups": runtime.half_groups,
                    "workspace_slots": len(set(runtime.block_slot.values())), **matvec_info},
         "uncompressed_tok_s": round(base_tok_s, 2),
         "ratio_vs_uncompressed": round(base_tok_s / tok_s, 3),

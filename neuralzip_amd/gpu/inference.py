@@ -536,6 +536,7 @@ class NeuralZipRuntime:
         decoded = sum(g.encoded.raw_bytes for g in exported.groups)
         half_groups = (self.prefetch and granularity == "block"
                        and decoded < HALF_GROUP_MAX_BYTES * max(len(order), 1))
+        self.half_groups = half_groups   # prefetches run as half-size workgroups
         cus = self._compute_units()
         for (name, dtype), frags in by_unit.items():
             spec = DTYPES[dtype]
