@@ -215,7 +215,7 @@ def test_block_launch_workgroups(decode_slots):
                                       decode_slots=decode_slots)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     resident = _native.decode_slots(2, 1, 0)
-    assert runtime.prefetch and runtime._ahead_batches is not runtime._prepared_batches
+    assert runtime.prefetch and runtime.half_groups and runtime._ahead_batches is not runtime._prepared_batches
     for plans, half in ((runtime._ahead_batches, True), (runtime._prepared_batches, False)):
         for batch in (b for batches in plans.values() for b in batches):
             assert bool(batch.launch_args[-1] & _native.DECODE_HALF_GROUPS) == half
@@ -241,7 +241,7 @@ def test_large_blocks_prefetch_with_full_workgroups(monkeypatch):
                                       device="cuda:0")
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     resident = _native.decode_slots(2, 1, 0)
-    assert runtime._ahead_batches is runtime._prepared_batches
+    assert not runtime.half_groups and runtime._ahead_batches is runtime._prepared_batches
     for batches in runtime._prepared_batches.values():
         for batch in batches:
             assert not batch.launch_args[-1] & _native.DECODE_HALF_GROUPS
