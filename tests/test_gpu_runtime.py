@@ -191,6 +191,65 @@ def test_graph_replays_match_eager(prefetch):
             assert exact(eager, _run(reference.blocks, inputs[(k + 1) % len(inputs)])), f"eager after replay {k}"
 
 
+class _MixedBlock(nn.Module):
+    """One Linear each in bf16, fp16 and fp32, the activations cast between."""
+
+    def __init__(self, width):
+        super().__init__()
+        self.a = nn.Linear(width, width, bias=False, dtype=torch.bfloat16)
+        self.b = nn.Linear(width, width, bias=False, dtype=torch.float16)
+        self.c = nn.Linear(width, width, bias=False, dtype=torch.float32)
+
+    def forward(self, x):
+        x = self.a(x.to(torch.bfloat16))
+        x = self.b(x.to(torch.float16))
+        return self.c(x.to(torch.float32))
+
+
+@pytest.mark.parametrize("prefetch", [True, None])
+def test_blocks_of_three_dtypes(prefetch):
+    """Blocks holding bf16, fp16 and fp32 weights: one workspace and one
+    launch plan per dtype and block, three slots, prefetches as half-size
+    workgroups. Eager forwards and graph replays (side-stream decodes
+    captured, or every decode on the compute stream) stay bitwise equal to
+    the uncompressed blocks, with eager forwards between replays."""
+    model = nn.Module()
+    model.blocks = nn.ModuleList([_MixedBlock(512) for _ in range(5)])
+    g = torch.Generator().manual_seed(23)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_((torch.randn(p.shape, generator=g) * 0.03).to(p.dtype))
+    named = {n: p.detach().clone() for n, p in model.named_parameters()}
+    reference = copy.deepcopy(model).cuda()
+    runtime = NeuralZipRuntime.attach(model, export_model_for_gpu(model, NeuralZipSetup(chunk_size=65536).build(named)),
+                                      device="cuda:0")
+    assert set(runtime.workspaces) == {torch.bfloat16, torch.float16, torch.float32}
+    assert runtime.half_groups and len(set(runtime.block_slot.values())) == 3
+    inputs = [torch.randn(8, 512, generator=g).cuda() for _ in range(3)]
+    with torch.no_grad():
+        expected = [_run(reference.blocks, x) for x in inputs]
+        for _ in range(2):
+            for x, want in zip(inputs, expected):
+                assert exact(_run(model.blocks, x), want)
+        static = inputs[0].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            _run(model.blocks, static)   # warm-up before the capture
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with runtime.graph_capture(prefetch), torch.cuda.graph(graph):
+            out = _run(model.blocks, static)
+        for k in range(6):
+            static.copy_(inputs[k % 3])
+            graph.replay()
+            got = out.clone()
+            eager = _run(model.blocks, inputs[(k + 1) % 3])
+            torch.cuda.synchronize()
+            assert exact(got, expected[k % 3]), f"replay {k}"
+            assert exact(eager, expected[(k + 1) % 3]), f"eager after replay {k}"
+
+
 @pytest.mark.parametrize("decode_slots", [None, 512, 3])
 def test_block_launch_workgroups(decode_slots):
     """Prefetches of small blocks use half-size workgroups (8 wavefronts),
