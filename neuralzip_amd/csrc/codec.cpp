@@ -723,7 +723,10 @@ static inline uint64_t load_be64(const uint8_t* p) {
 // multi-token table where they fit the lane's counts; anything else (codes
 // over 12 bits, a lane's last tokens, a frame that runs short) takes one
 // token at a time.
-void nzm1_decode(const Codebook& book, const uint8_t* src, size_t size, uint8_t* dst, size_t n) {
+// NZM1 frame decode, one lane after the other, every check in the
+// reference's order (mixed_huffman.h:180-240): the canonical decode, and the
+// one whose first error a corrupt frame reports.
+static void nzm1_decode_sequential(const Codebook& book, const uint8_t* src, size_t size, uint8_t* dst, size_t n) {
     if (size < 32) fail(kCorruptStream, "Truncated mixed Huffman frame.");
     size_t cursor = 32, written = 0;
     thread_local std::vector<uint8_t> lane_buf;
@@ -767,6 +770,110 @@ void nzm1_decode(const Codebook& book, const uint8_t* src, size_t size, uint8_t*
         cursor += bytes;
     }
     if (cursor != size || written != n) fail(kCorruptStream, "Mixed decoded size mismatch.");
+}
+
+// The same decode with the four lanes interleaved. The lanes are independent
+// bit streams (each one's codes restart at its own first bit), so one table
+// step of each lane in turn keeps four dependency chains in flight instead of
+// one. A lane's output starts after the bytes of the lanes before it, which
+// pair tokens make unknown until those are decoded: lane 0 decodes into
+// `dst`, lanes 1-3 into scratch that is moved behind it afterwards. A frame
+// that fails any check is decoded again by nzm1_decode_sequential, so that it
+// reports the same first error.
+void nzm1_decode(const Codebook& book, const uint8_t* src, size_t size, uint8_t* dst, size_t n) {
+    if (size < 32) fail(kCorruptStream, "Truncated mixed Huffman frame.");
+    struct Lane {
+        const uint8_t* bits = nullptr;   // the lane, then zero padding
+        uint64_t n_bits = 0, pos = 0;
+        uint32_t left = 0;               // tokens still to decode
+        uint8_t* out = nullptr;
+        size_t written = 0, room = 0;    // bytes written; bytes the lane may write
+    };
+    Lane lanes[4];
+    size_t lane_bytes[4];
+    bool clean = true;
+    size_t cursor = 32, tokens_total = 0;
+    for (unsigned k = 0; k < 4 && clean; ++k) {
+        uint32_t tokens = 0, bits = 0;
+        for (int b = 0; b < 4; ++b) {
+            tokens |= uint32_t(src[8 * k + b]) << (8 * b);
+            bits |= uint32_t(src[8 * k + 4 + b]) << (8 * b);
+        }
+        lane_bytes[k] = (uint64_t(bits) + 7) / 8;
+        clean = lane_bytes[k] <= size - cursor && tokens <= n - tokens_total;
+        lanes[k].n_bits = bits;
+        lanes[k].left = tokens;
+        cursor += clean ? lane_bytes[k] : 0;
+        tokens_total += tokens;
+    }
+    if (!clean || cursor != size) return nzm1_decode_sequential(book, src, size, dst, n);
+    thread_local std::vector<uint8_t> lane_buf, out_buf;
+    size_t padded = 0;
+    for (unsigned k = 0; k < 4; ++k) padded += lane_bytes[k] + 16;   // an 8-byte read below n_bits stays inside
+    lane_buf.assign(padded, 0);
+    for (size_t k = 0, at = 32, off = 0; k < 4; ++k) {
+        std::memcpy(lane_buf.data() + off, src + at, lane_bytes[k]);
+        lanes[k].bits = lane_buf.data() + off;
+        at += lane_bytes[k];
+        off += lane_bytes[k] + 16;
+    }
+    // Lane 0 writes into dst (at most n bytes); lanes 1-3 into scratch of
+    // their tokens' largest expansion plus the 4 bytes a 4-byte store may
+    // write past its last byte.
+    size_t scratch = 0;
+    for (unsigned k = 1; k < 4; ++k) scratch += 2 * size_t(lanes[k].left) + 4;
+    out_buf.resize(scratch);
+    lanes[0].out = dst;
+    lanes[0].room = n;
+    for (size_t k = 1, at = 0; k < 4; ++k) {
+        lanes[k].out = out_buf.data() + at;
+        lanes[k].room = 2 * size_t(lanes[k].left);
+        at += lanes[k].room + 4;
+    }
+    const uint64_t* multi = book.multi.data();
+    // One step of lane L: a whole table entry when it fits the lane's tokens,
+    // bits and output room (a 4-byte store needs 4 bytes: scratch lanes have
+    // them past `room`, lane 0 checks), else the checked single-token step.
+    // Returns false on a corrupt stream.
+    auto step = [&](Lane& L, bool store_slack) {
+        const uint64_t window = load_be64(L.bits + (L.pos >> 3)) << (L.pos & 7);   // >= 57 valid bits
+        const uint64_t e = multi[window >> (64 - NZ_LUT_BITS)];
+        if (e && multi_tokens(e) <= L.left && L.pos + multi_bits(e) <= L.n_bits &&
+            (store_slack || L.room - L.written >= 4)) {
+            store32(L.out + L.written, static_cast<uint32_t>(e));
+            L.written += multi_bytes(e);
+            L.pos += multi_bits(e);
+            L.left -= multi_tokens(e);
+            return true;
+        }
+        if (L.pos >= L.n_bits) return false;
+        uint32_t value;
+        unsigned count;
+        const unsigned len = token_step(book, window, &value, &count);
+        if (L.pos + len > L.n_bits || count > L.room - L.written) return false;
+        for (unsigned b = 0; b < count; ++b) L.out[L.written++] = static_cast<uint8_t>(value >> (8 * b));
+        L.pos += len;
+        --L.left;
+        return true;
+    };
+    try {
+        while (clean && lanes[0].left && lanes[1].left && lanes[2].left && lanes[3].left)
+            clean = step(lanes[0], false) && step(lanes[1], true) && step(lanes[2], true) && step(lanes[3], true);
+        for (unsigned k = 0; k < 4 && clean; ++k)
+            while (clean && lanes[k].left) clean = step(lanes[k], k != 0);
+    } catch (const Error&) {   // token_step's own checks
+        clean = false;
+    }
+    size_t written = 0;
+    for (size_t k = 0, at = 32; k < 4 && clean; ++k) {
+        const uint64_t bits = lanes[k].n_bits;
+        clean = lanes[k].pos == bits && lanes[k].written <= n - written &&
+                !(bits % 8 && (src[at + lane_bytes[k] - 1] & ((1u << (8 - bits % 8)) - 1)));
+        if (clean && k) std::memcpy(dst + written, lanes[k].out, lanes[k].written);
+        written += lanes[k].written;
+        at += lane_bytes[k];
+    }
+    if (!clean || written != n) return nzm1_decode_sequential(book, src, size, dst, n);
 }
 
 }  // namespace nz

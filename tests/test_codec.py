@@ -137,6 +137,27 @@ def test_nzm1_frames_cross_decode(max_bits):
     assert huff0.decode_block(book, frame, len(symbols)) == symbols
 
 
+@pytest.mark.parametrize("max_bits", [12, 56])
+def test_nzm1_lanes_of_every_small_size_decode(max_bits):
+    """The product decodes the four lanes of an NZM1 frame interleaved and
+    finishes each lane alone once any lane runs out. Frames of 0-40 symbols
+    (lanes of zero, one or a few tokens), pairs straddling the lane splits
+    and long codes, written by the oracle's encoder, decode to their
+    symbols."""
+    from nz_helpers import segment_lengths
+    vocab = bytes((127, 127, 125, 126))
+    header = b"NZM1" + segment_lengths(max_bits)
+    book = huff0.build_codebook_from_header(header, vocab=vocab)
+    table = oracle.MixedTable(header, vocab)
+    rng = np.random.default_rng(max_bits)
+    alphabet = np.array([127, 127, 127, 125, 126, 0, 200, 255], dtype=np.uint8)
+    for n in range(41):
+        for _ in range(3):
+            symbols = bytes(rng.choice(alphabet, n))
+            frame = table.encode(symbols)
+            assert huff0.decode_block(book, frame, n) == symbols, (n, symbols)
+
+
 def test_build_mixed_codebook_matches_oracle_heap():
     rng = np.random.default_rng(0)
     for _ in range(10):
